@@ -1,0 +1,225 @@
+/*
+ * paged_attn.h -- C-ABI of libpa_hip.so, the MI355X (gfx950) paged-attention backend.
+ *
+ * The reference framework (werwedc/ml-framework, C#/.NET) reaches native code only through
+ * P/Invoke declarations with CallingConvention.Cdecl into libraries it does not ship:
+ *   - the CUDA runtime surface of its HAL   src/MLFramework/HAL/CUDA/CudaApi.cs:9-269
+ *   - its custom-kernel library             src/MLFramework/HAL/CUDA/CudaKernels.cs:10-141
+ *   - the paged-attention operator stub     src/MLFramework/Inference/PagedAttention/Kernels/
+ *                                           CudaPagedAttentionKernel.cs:11-49 (throws)
+ * Every entry point below replaces one of those declarations (cited per function) or fills the
+ * operator stub. All functions are extern "C", take plain pointers and sizes, return a pa_status
+ * (0 = success) and never throw. Launch functions validate their arguments on the host and return
+ * an error without launching anything when a check fails. Device pointers are owned by the
+ * caller; the library never frees memory it did not allocate through pa_alloc.
+ *
+ * Threading: launch functions are asynchronous on the given stream and return after enqueue. The
+ * library keeps no mutable global state except a thread-local last-error string, so one pa_device
+ * may be driven from several host threads, each with its own stream.
+ */
+#ifndef PAGED_ATTN_H
+#define PAGED_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_API_VERSION_MAJOR 1
+#define PA_API_VERSION_MINOR 0
+
+/* Status codes. Mirrors the integer-error-to-exception mapping of the reference HAL
+ * (src/MLFramework/HAL/CUDA/CudaError.cs, CudaException.CheckError used at CudaDevice.cs:15-21). */
+typedef enum pa_status {
+    PA_SUCCESS = 0,
+    PA_ERROR_INVALID_ARGUMENT = 1,   /* null pointer, negative count, out-of-range value      */
+    PA_ERROR_INVALID_CONFIG = 2,     /* pa_config inconsistent (heads, head_dim, block size)  */
+    PA_ERROR_OUT_OF_MEMORY = 3,      /* device allocation failed                              */
+    PA_ERROR_HIP = 4,                /* a HIP runtime call failed; see pa_get_last_error      */
+    PA_ERROR_UNSUPPORTED = 5,        /* dtype / head_dim / GQA ratio not compiled             */
+    PA_ERROR_WORKSPACE_TOO_SMALL = 6,/* caller workspace smaller than pa_*_workspace_size     */
+    PA_ERROR_NO_DEVICE = 7           /* no HIP device with that ordinal                       */
+} pa_status;
+
+/* Element types. Values follow the order of MLFramework.Core.DataType only where they coincide
+ * (src/MLFramework/Core/DataType.cs:6-21); the ABI fixes its own numbering. */
+typedef enum pa_dtype {
+    PA_DTYPE_FP32 = 0,
+    PA_DTYPE_BF16 = 1,   /* stored as the upper 16 bits of fp32 (truncating conversion,
+                            src/MLFramework/Amp/BFloat16.cs:99-117)                              */
+    PA_DTYPE_INT8 = 2    /* symmetric int8 with an fp32 scale per (block, KV head)            */
+} pa_dtype;
+
+/* Attention phase, numbered as MlFramework.Inference.PagedAttention.Phases.AttentionPhase
+ * (Phases/AttentionPhase.cs:6-17): Prefill = 0, Decode = 1. */
+typedef enum pa_phase { PA_PHASE_PREFILL = 0, PA_PHASE_DECODE = 1 } pa_phase;
+
+/* pa_config.flags */
+#define PA_FLAG_NONE 0u
+/* Chunked prefill: apply the reference's mask rule literally (mask only when phase == Decode and
+ * the number of cached keys exceeds the number of queries, StandardPagedAttentionKernel.cs:57),
+ * i.e. no mask when the prefix is empty or the phase is Prefill. Default: always causal. */
+#define PA_FLAG_REFERENCE_LITERAL_MASK 1u
+/* Chunked prefill: no mask at all -- the reference's Prefill phase, used by the dense
+ * IPagedAttentionKernel interface when called with AttentionPhase.Prefill. */
+#define PA_FLAG_NO_MASK 2u
+
+/* Shape/dtype record passed by pointer to every launch function.
+ * KV cache layout (per layer, K and V separately): [num_blocks][num_kv_heads][block_size][head_dim]
+ * of kv_dtype -- the reference's intended per-block tensor [layers, heads, blockSize, headDim]
+ * (src/MLFramework/Inference/PagedAttention/Layers/PagedAttentionLayer.cs:315) for one layer.
+ * int8 scales and running absolute maxima: fp32 [num_blocks][num_kv_heads], K and V separately. */
+typedef struct pa_config {
+    int32_t block_size;     /* tokens per physical block; 16 in every shipped configuration    */
+    int32_t num_q_heads;    /* Hq                                                               */
+    int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, query head h reads KV head h / (Hq / Hkv)    */
+    int32_t head_dim;       /* D: 64, 128 or 256                                                */
+    int32_t kv_dtype;       /* pa_dtype of the cache                                            */
+    int32_t q_dtype;        /* pa_dtype of Q and of the new K/V handed to pa_kv_append (FP32/BF16) */
+    int32_t num_blocks;     /* physical blocks in the pool; ids outside [0, num_blocks) are
+                               never dereferenced (their tokens are skipped)                    */
+    float   scale;          /* softmax scale; <= 0 selects 1/sqrtf(head_dim)
+                               (StandardPagedAttentionKernel.cs:18,28)                          */
+    int32_t partition_size; /* decode split-K partition length in tokens; 0 = library default  */
+    uint32_t flags;         /* PA_FLAG_*                                                        */
+} pa_config;
+
+typedef struct pa_device pa_device;
+typedef struct pa_stream pa_stream;
+typedef struct pa_event pa_event;
+
+typedef struct pa_device_props {
+    char name[256];
+    char arch[64];             /* e.g. "gfx950:sramecc+:xnack-" */
+    size_t total_memory;
+    int32_t compute_units;
+    int32_t ordinal;
+} pa_device_props;
+
+typedef enum pa_memcpy_kind {
+    PA_MEMCPY_HOST_TO_HOST = 0,
+    PA_MEMCPY_HOST_TO_DEVICE = 1,
+    PA_MEMCPY_DEVICE_TO_HOST = 2,
+    PA_MEMCPY_DEVICE_TO_DEVICE = 3,
+    PA_MEMCPY_DEFAULT = 4
+} pa_memcpy_kind;
+
+/* ---- library / errors --------------------------------------------------------------------- */
+pa_status pa_get_version(int32_t* major, int32_t* minor);
+const char* pa_status_string(pa_status status);
+/* Copies the calling thread's last error message (NUL-terminated, truncated to buf_len). */
+pa_status pa_get_last_error(char* buf, size_t buf_len);
+
+/* ---- device (replaces CudaApi.CudaGetDeviceCount/CudaSetDevice/CudaGetDeviceProperties/
+ *      CudaDeviceSynchronize, CudaApi.cs:18-37;
+ *      backs IDevice, src/MLFramework/HAL/IDevice.cs:6-42) ------------------------------------ */
+pa_status pa_device_count(int32_t* count);
+pa_status pa_device_open(int32_t ordinal, pa_device** out_device);
+pa_status pa_device_close(pa_device* device);
+pa_status pa_device_get_props(const pa_device* device, pa_device_props* props);
+pa_status pa_device_synchronize(pa_device* device);
+
+/* ---- memory (replaces CudaApi.CudaMalloc/CudaFree/CudaMemcpy/CudaMemset, CudaApi.cs:46-75;
+ *      backs IMemoryAllocator/IMemoryBuffer, HAL/IMemoryAllocator.cs:6-43) ------------------- */
+pa_status pa_alloc(pa_device* device, size_t bytes, void** dptr);
+pa_status pa_free(pa_device* device, void* dptr);
+/* Asynchronous on `stream` when it is non-null, otherwise synchronous. */
+pa_status pa_memcpy(void* dst, const void* src, size_t bytes, int32_t kind, pa_stream* stream);
+pa_status pa_memset(void* dst, int32_t value, size_t bytes, pa_stream* stream);
+
+/* ---- streams and events (replace CudaApi.CudaStreamCreate/Destroy/Synchronize and
+ *      CudaEventCreate/Destroy/Record/Query and CudaStreamWaitEvent, CudaApi.cs:81-128;
+ *      back IStream/IEvent, HAL/IStream.cs:6-32, HAL/IEvent.cs:6-22) ---------------------- */
+pa_status pa_stream_create(pa_device* device, pa_stream** out_stream);
+/* Wraps an existing hipStream_t without taking ownership (interop with other HIP users). */
+pa_status pa_stream_wrap(pa_device* device, void* hip_stream, pa_stream** out_stream);
+pa_status pa_stream_native(const pa_stream* stream, void** hip_stream);
+pa_status pa_stream_destroy(pa_stream* stream);
+pa_status pa_stream_synchronize(pa_stream* stream);
+pa_status pa_stream_wait_event(pa_stream* stream, pa_event* event);
+pa_status pa_event_create(pa_device* device, pa_event** out_event);
+pa_status pa_event_destroy(pa_event* event);
+pa_status pa_event_record(pa_event* event, pa_stream* stream);
+pa_status pa_event_query(pa_event* event, int32_t* completed);
+pa_status pa_event_synchronize(pa_event* event);
+pa_status pa_event_elapsed_ms(pa_event* start, pa_event* end, float* ms);
+
+/* ---- paged-attention operators (fill CudaPagedAttentionKernel.ComputePagedAttention,
+ *      CudaPagedAttentionKernel.cs:24-36, behind IPagedAttentionKernel,
+ *      Kernels/IPagedAttentionKernel.cs:11-34) ------------------------------------------------ */
+
+/* Slot mapping for new tokens (device arrays). For sequence s, new token j (0 <= j < num_new[s])
+ * sits at logical position p = start_pos[s] + j and gets
+ *     slot_mapping[token_offset[s] + j] = block_tables[s][p / B] * B + p % B,
+ * or -1 when that table entry is negative or p / B >= max_blocks_per_seq. This is the intended
+ * BlockTable mapping (block k of a sequence holds tokens [k*B, (k+1)*B),
+ * tests/MLFramework.Tests/Inference/PagedAttention/BlockTableTests.cs:115-134) combined with the
+ * append position of PagedAttentionLayer.UpdateKVCache (Layers/PagedAttentionLayer.cs:256-272). */
+pa_status pa_build_slot_mapping(pa_stream* stream, const pa_config* cfg,
+                                const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                const int32_t* start_pos, const int32_t* num_new,
+                                const int32_t* token_offset, int32_t num_seqs,
+                                int32_t max_new_per_seq, int64_t* slot_mapping);
+
+/* KV append / scatter (fills PagedAttentionLayer.UpdateKVCache/CopyTensorToBlock,
+ * Layers/PagedAttentionLayer.cs:244-327, which is a no-op in the reference).
+ * k_new, v_new: [n_tok][num_kv_heads][head_dim] of cfg->q_dtype (FP32 or BF16).
+ * slot_mapping: [n_tok] int64, -1 = skip. Slots must be < num_blocks * block_size.
+ * FP32/BF16 caches store the converted value (fp32 -> bf16 truncates).
+ * INT8 caches keep, per (block, KV head), an fp32 running absmax and scale = absmax / 127.
+ *   Per call, the new tokens of one block raise absmax to max(absmax, max|x_new|); when it grows,
+ *   every other slot of that block is requantised from q * old_scale with the new scale, then
+ *   the new tokens are quantised with it. Quantisation is QuantizeSymmetric
+ *   (src/MLFramework/Quantization/Operations/QuantizationOperations.cs:188-200).
+ *   All new tokens that land in one block must be consecutive in the token list of a call.
+ *   k_scale/v_scale/k_absmax/v_absmax are required for INT8 and ignored otherwise. */
+pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg,
+                       const void* k_new, const void* v_new,
+                       const int64_t* slot_mapping, int32_t n_tok,
+                       void* k_cache, void* v_cache,
+                       float* k_scale, float* v_scale, float* k_absmax, float* v_absmax);
+
+/* Bytes of device workspace pa_paged_decode needs for this shape (0 when no sequence needs more
+ * than one partition). */
+pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs,
+                                   int32_t max_context_len, size_t* bytes);
+
+/* Ragged paged decode: one query token per sequence attends to its first context_lens[s] cached
+ * tokens (the new token already appended), as DecodeOrchestrator.BatchDecode does with one
+ * kernel call per sequence (Phases/DecodeOrchestrator.cs:64-109).
+ *   out: [num_seqs][num_q_heads][head_dim] fp32
+ *   q:   [num_seqs][num_q_heads][head_dim] of cfg->q_dtype
+ *   block_tables: [num_seqs][max_blocks_per_seq] int32, context_lens: [num_seqs] int32
+ *   max_context_len: host-side upper bound of context_lens (sizes the grid); tokens beyond it,
+ *   or beyond max_blocks_per_seq * block_size, are not read.
+ * Sequences longer than one partition (cfg->partition_size) are split across workgroups and
+ * merged with a log-sum-exp reduction through `workspace`. A sequence with context_len <= 0
+ * produces zeros. */
+pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                          const void* k_cache, const void* v_cache,
+                          const float* k_scale, const float* v_scale,
+                          const int32_t* block_tables, const int32_t* context_lens,
+                          int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
+                          void* workspace, size_t workspace_bytes);
+
+/* Chunked prefill: prefill sequence s has chunk_len[s] = q_start_loc[s+1] - q_start_loc[s] new
+ * query tokens at absolute positions prefix_lens[s] + i; the chunk's K/V must already be appended,
+ * so keys are positions [0, prefix_lens[s] + chunk_len[s]) read through block_tables[s].
+ * Query i attends to keys 0 .. prefix_lens[s] + i (bottom-right aligned causal mask,
+ * StandardPagedAttentionKernel.cs:219-255); see PA_FLAG_REFERENCE_LITERAL_MASK.
+ *   out: [total_q][num_q_heads][head_dim] fp32, q: [total_q][num_q_heads][head_dim] BF16.
+ *   max_chunk_len: host-side upper bound of the chunk lengths. */
+pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                             const int32_t* q_start_loc, const int32_t* prefix_lens,
+                             const void* k_cache, const void* v_cache,
+                             const float* k_scale, const float* v_scale,
+                             const int32_t* block_tables, int32_t num_seqs,
+                             int32_t max_blocks_per_seq, int32_t max_chunk_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_ATTN_H */

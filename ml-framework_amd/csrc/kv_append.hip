@@ -1,0 +1,224 @@
+// kv_append.hip -- slot mapping and KV-cache append/scatter for gfx950.
+//
+// Fills the no-op placeholders of the reference's append path: PagedAttentionLayer.UpdateKVCache /
+// CopyTensorToBlock (src/MLFramework/Inference/PagedAttention/Layers/PagedAttentionLayer.cs:244-327).
+// Cache layout per layer: [num_blocks][num_kv_heads][16][head_dim] (PagedAttentionLayer.cs:315 for
+// one layer). Both kernels are HBM-bound scatters; the int8 one also owns the per-(block, KV head)
+// scale and running absmax.
+#include <string>
+
+#include "pa_internal.h"
+
+namespace {
+
+// Slot of new token j of sequence s: table[s][p / 16] * 16 + p % 16 with p = start_pos[s] + j.
+__global__ __launch_bounds__(256) void slot_mapping_kernel(
+    const int32_t* __restrict__ block_tables, int32_t max_blocks_per_seq,
+    const int32_t* __restrict__ start_pos, const int32_t* __restrict__ num_new,
+    const int32_t* __restrict__ token_offset, int64_t* __restrict__ slot_mapping) {
+    const int s = blockIdx.x;
+    const int n = num_new[s];
+    const int64_t p0 = start_pos[s];
+    const int64_t dst0 = token_offset[s];
+    for (int j = blockIdx.y * blockDim.x + threadIdx.x; j < n; j += gridDim.y * blockDim.x) {
+        const int64_t p = p0 + j;
+        const int64_t lb = p / pa::kBlockSize;
+        int64_t slot = -1;
+        if (p >= 0 && lb < max_blocks_per_seq) {
+            const int32_t blk = block_tables[static_cast<int64_t>(s) * max_blocks_per_seq + lb];
+            if (blk >= 0) slot = static_cast<int64_t>(blk) * pa::kBlockSize + p % pa::kBlockSize;
+        }
+        slot_mapping[dst0 + j] = slot;
+    }
+}
+
+__device__ __forceinline__ float load_act(const void* p, bool bf16, int64_t i) {
+    return bf16 ? pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+// fp32 / bf16 caches: one workgroup per token, blockIdx.y selects K (0) or V (1).
+__global__ __launch_bounds__(256) void append_plain_kernel(
+    const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
+    const int64_t* __restrict__ slot_mapping, void* __restrict__ k_cache, void* __restrict__ v_cache,
+    bool cache_bf16, int32_t num_kv_heads, int32_t head_dim, int64_t capacity) {
+    const int i = blockIdx.x;
+    const int64_t slot = slot_mapping[i];
+    if (slot < 0 || slot >= capacity) return;
+    const void* src = blockIdx.y == 0 ? k_new : v_new;
+    void* dst = blockIdx.y == 0 ? k_cache : v_cache;
+    const int64_t blk = slot / pa::kBlockSize, off = slot % pa::kBlockSize;
+    const int n = num_kv_heads * head_dim;
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        const int h = idx / head_dim, d = idx - h * head_dim;
+        const float x = load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
+        const int64_t o = ((blk * num_kv_heads + h) * pa::kBlockSize + off) * head_dim + d;
+        if (cache_bf16) static_cast<uint16_t*>(dst)[o] = pa::bf16_trunc(x);
+        else static_cast<float*>(dst)[o] = x;
+    }
+}
+
+// int8 caches: one wave per (token, KV head, K|V). Only the wave of the first token of a run of
+// consecutive tokens that land in the same block (a "segment") does work; it owns that
+// (block, head) for the call, so no two waves touch one block's codes or scale.
+template <int D>
+__global__ __launch_bounds__(64) void append_int8_kernel(
+    const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
+    const int64_t* __restrict__ slot_mapping, int32_t n_tok, int8_t* __restrict__ k_cache,
+    int8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    float* __restrict__ k_absmax, float* __restrict__ v_absmax, int32_t num_kv_heads, int64_t capacity) {
+#pragma clang fp contract(off)
+    constexpr int kPer = D / 64;  // elements per lane
+    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const bool is_v = blockIdx.z != 0;
+    const void* src = is_v ? v_new : k_new;
+    int8_t* cache = is_v ? v_cache : k_cache;
+    float* scale = is_v ? v_scale : k_scale;
+    float* absmax = is_v ? v_absmax : k_absmax;
+
+    const int64_t slot = slot_mapping[i];
+    if (slot < 0 || slot >= capacity) return;
+    const int64_t blk = slot / pa::kBlockSize;
+    if (i > 0) {
+        const int64_t prev = slot_mapping[i - 1];
+        if (prev >= 0 && prev < capacity && prev / pa::kBlockSize == blk) return;  // not a segment head
+    }
+    // Extent of the segment, the slots it writes and the absmax of its values for head h.
+    int end = i;
+    uint32_t written = 0;
+    bool fresh = false;
+    float seg_amax = 0.0f;
+    while (end < n_tok) {
+        const int64_t s = slot_mapping[end];
+        if (s < 0 || s >= capacity || s / pa::kBlockSize != blk) break;
+        const int off = static_cast<int>(s % pa::kBlockSize);
+        written |= 1u << off;
+        fresh |= off == 0;
+        const int64_t base = (static_cast<int64_t>(end) * num_kv_heads + h) * D;
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            const float a = fabsf(load_act(src, in_bf16, base + lane + 64 * k));
+            seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
+        }
+        end++;
+    }
+    seg_amax = pa::wave_max(seg_amax);
+
+    const int64_t sidx = blk * num_kv_heads + h;
+    int8_t* block_codes = cache + ((blk * num_kv_heads + h) * pa::kBlockSize) * D;
+    float cur_scale;
+    if (fresh) {
+        // Writing row 0 starts the block: earlier contents and statistics are discarded.
+        cur_scale = seg_amax / 127.0f;
+        if (lane == 0) {
+            absmax[sidx] = seg_amax;
+            scale[sidx] = cur_scale;
+        }
+    } else {
+        const float old_amax = absmax[sidx];
+        const float old_scale = scale[sidx];
+        cur_scale = old_scale;
+        if (seg_amax > old_amax) {
+            cur_scale = seg_amax / 127.0f;
+            // Requantise every row this segment does not overwrite:
+            // QuantizeSymmetric(Dequantize(q, old_scale), new_scale).
+            for (int off = 0; off < pa::kBlockSize; off++) {
+                if (written & (1u << off)) continue;
+#pragma unroll
+                for (int k = 0; k < kPer; k++) {
+                    int8_t* c = block_codes + off * D + lane + 64 * k;
+                    const float deq = static_cast<float>(static_cast<int32_t>(*c)) * old_scale;
+                    *c = pa::quantize_symmetric(deq, cur_scale);
+                }
+            }
+            if (lane == 0) {
+                absmax[sidx] = seg_amax;
+                scale[sidx] = cur_scale;
+            }
+        }
+    }
+    for (int t = i; t < end; t++) {
+        const int off = static_cast<int>(slot_mapping[t] % pa::kBlockSize);
+        const int64_t base = (static_cast<int64_t>(t) * num_kv_heads + h) * D;
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            const float x = load_act(src, in_bf16, base + lane + 64 * k);
+            block_codes[off * D + lane + 64 * k] = pa::quantize_symmetric(x, cur_scale);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+pa_status pa_build_slot_mapping(pa_stream* stream, const pa_config* cfg,
+                                const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                const int32_t* start_pos, const int32_t* num_new,
+                                const int32_t* token_offset, int32_t num_seqs,
+                                int32_t max_new_per_seq, int64_t* slot_mapping) {
+    if (!cfg) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_build_slot_mapping: cfg is null");
+    if (cfg->block_size != pa::kBlockSize)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_build_slot_mapping: block_size must be 16");
+    if (num_seqs < 0 || max_blocks_per_seq < 0 || max_new_per_seq < 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_build_slot_mapping: negative size");
+    if (num_seqs == 0 || max_new_per_seq == 0) return pa::clear_error();
+    if (!block_tables || !start_pos || !num_new || !token_offset || !slot_mapping)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_build_slot_mapping: null pointer");
+    const int per = 256;
+    int gy = (max_new_per_seq + per - 1) / per;
+    if (gy > 65535) gy = 65535;
+    dim3 grid(num_seqs, gy);
+    slot_mapping_kernel<<<grid, per, 0, pa::native(stream)>>>(block_tables, max_blocks_per_seq, start_pos,
+                                                              num_new, token_offset, slot_mapping);
+    PA_HIP_CHECK(hipGetLastError());
+    return pa::clear_error();
+}
+
+pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg, const void* k_new, const void* v_new,
+                       const int64_t* slot_mapping, int32_t n_tok, void* k_cache, void* v_cache,
+                       float* k_scale, float* v_scale, float* k_absmax, float* v_absmax) {
+    pa_status st = pa::check_config(cfg, "pa_kv_append");
+    if (st != PA_SUCCESS) return st;
+    if (n_tok < 0) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: n_tok < 0");
+    if (n_tok == 0) return pa::clear_error();
+    if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: null pointer");
+    const int64_t capacity = static_cast<int64_t>(cfg->num_blocks) * pa::kBlockSize;
+    const bool in_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
+    hipStream_t s = pa::native(stream);
+    if (cfg->kv_dtype != PA_DTYPE_INT8) {
+        dim3 grid(n_tok, 2);
+        append_plain_kernel<<<grid, 256, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, k_cache, v_cache,
+                                                  cfg->kv_dtype == PA_DTYPE_BF16, cfg->num_kv_heads,
+                                                  cfg->head_dim, capacity);
+    } else {
+        if (!k_scale || !v_scale || !k_absmax || !v_absmax)
+            return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: int8 cache needs scales and absmax");
+        if (cfg->num_kv_heads > 65535)
+            return pa::set_error(PA_ERROR_INVALID_CONFIG, "pa_kv_append: too many KV heads");
+        dim3 grid(n_tok, cfg->num_kv_heads, 2);
+        auto* kc = static_cast<int8_t*>(k_cache);
+        auto* vc = static_cast<int8_t*>(v_cache);
+        switch (cfg->head_dim) {
+            case 64:
+                append_int8_kernel<64><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                           k_scale, v_scale, k_absmax, v_absmax,
+                                                           cfg->num_kv_heads, capacity);
+                break;
+            case 128:
+                append_int8_kernel<128><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                            k_scale, v_scale, k_absmax, v_absmax,
+                                                            cfg->num_kv_heads, capacity);
+                break;
+            default:
+                append_int8_kernel<256><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                            k_scale, v_scale, k_absmax, v_absmax,
+                                                            cfg->num_kv_heads, capacity);
+                break;
+        }
+    }
+    PA_HIP_CHECK(hipGetLastError());
+    return pa::clear_error();
+}
+
+}  // extern "C"

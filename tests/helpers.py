@@ -1,0 +1,85 @@
+"""Shared helpers of the test-suite: device buffers, the C-ABI calls with torch-backed memory,
+oracle-built int8 caches and the tolerance check."""
+from __future__ import annotations
+
+import numpy as np
+
+import paged_attention as pa
+
+BLOCK = 16
+
+# Tolerances of the parity bar: |gpu - oracle| <= atol + rtol * |oracle|, fp32 accumulation.
+TOL_BF16 = dict(atol=2e-3, rtol=1e-2)
+TOL_FP32 = dict(atol=2e-3, rtol=1e-2)
+TOL_INT8 = dict(atol=2e-2, rtol=1e-2)
+
+
+def tol_for(kv_dtype):
+    return {0: TOL_FP32, 1: TOL_BF16, 2: TOL_INT8}[kv_dtype]
+
+
+def cuda():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    return torch.device("cuda:0")
+
+
+_NP2TORCH = None
+
+
+def to_gpu(a: np.ndarray):
+    """Copies a numpy array to the GPU keeping its bytes (uint16 travels as int16)."""
+    import torch
+
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a.copy()).to(cuda())
+
+
+def to_np(t, dtype=None) -> np.ndarray:
+    a = t.detach().cpu().numpy()
+    if dtype is not None:
+        a = a.view(dtype)
+    return a
+
+
+def empty_gpu(shape, np_dtype):
+    import torch
+
+    tdt = {np.float32: torch.float32, np.int8: torch.int8, np.uint16: torch.int16,
+           np.int16: torch.int16, np.int32: torch.int32, np.int64: torch.int64,
+           np.uint8: torch.uint8}[np.dtype(np_dtype).type]
+    return torch.zeros(shape, dtype=tdt, device=cuda())
+
+
+def check_close(got: np.ndarray, ref: np.ndarray, atol: float, rtol: float, what: str = ""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(f"{what}: {bad.sum()} elements out of tolerance (atol={atol}, rtol={rtol}); "
+                             f"worst at {i}: got {got[i]}, ref {ref[i]}, max-abs {err.max():.3e}")
+    return float(err.max())
+
+
+def full_pool_slots(num_blocks):
+    """slot_mapping that appends every row of every block, block by block."""
+    return np.arange(num_blocks * BLOCK, dtype=np.int64)
+
+
+def pool_tokens(src: np.ndarray) -> np.ndarray:
+    """[nb][Hkv][16][D] source rows -> [nb*16][Hkv][D] token-major append input."""
+    nb, hkv, b, d = src.shape
+    return np.ascontiguousarray(src.transpose(0, 2, 1, 3).reshape(nb * b, hkv, d))
+
+
+def config_for(w, **kw):
+    return pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                          kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks, **kw)

@@ -1,0 +1,214 @@
+"""GPU parity of libpa_hip.so against the CPU oracle, called through the C-ABI.
+
+Bar: slot mapping, fp32/bf16 stores and int8 codes/scales/absmax are bit-exact; attention
+outputs satisfy |gpu - oracle| <= atol + rtol*|oracle| with (2e-3, 1e-2) for fp32/bf16 KV and
+(2e-2, 1e-2) for int8 KV (tests/helpers.py), accumulation in fp32.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import paged_attention as pa
+import pa_oracle as orc
+import workloads as wl
+from helpers import (check_close, config_for, empty_gpu, full_pool_slots, pool_tokens, to_gpu, to_np,
+                     tol_for)
+
+pytestmark = pytest.mark.gpu
+NTHREADS = min(16, os.cpu_count() or 1)
+
+
+@pytest.fixture(scope="module")
+def stream():
+    import torch
+
+    torch.cuda.init()
+    s = pa.TorchStream.current(0)
+    yield s.stream
+    s.stream.destroy()
+    s.device.close()
+
+
+def _sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def build_int8_caches(w, inp, stream):
+    """Quantises the fp32 source pool with the oracle and with the GPU append; they must agree."""
+    cfg = config_for(w)
+    nb, hkv, d = w.num_blocks, w.num_kv_heads, w.head_dim
+    slots = full_pool_slots(nb)
+    k_tok, v_tok = pool_tokens(inp["k_src"]), pool_tokens(inp["v_src"])
+    if w.q_dtype == 1:
+        k_tok, v_tok = orc.bf16_from_f32(k_tok), orc.bf16_from_f32(v_tok)
+    kc = np.zeros((nb, hkv, 16, d), np.int8)
+    vc = np.zeros_like(kc)
+    ks, vs, ka, va = (np.zeros((nb, hkv), np.float32) for _ in range(4))
+    orc.kv_append(cfg, k_tok, v_tok, slots, kc, vc, ks, vs, ka, va)
+    g = {n: empty_gpu(a.shape, a.dtype) for n, a in
+         dict(kc=kc, vc=vc, ks=ks, vs=vs, ka=ka, va=va).items()}
+    gk, gv, gsl = to_gpu(k_tok), to_gpu(v_tok), to_gpu(slots)
+    pa.kv_append(stream, cfg, gk, gv, gsl, len(slots), g["kc"], g["vc"], g["ks"], g["vs"], g["ka"], g["va"])
+    _sync()
+    for n, a in dict(kc=kc, vc=vc, ks=ks, vs=vs, ka=ka, va=va).items():
+        np.testing.assert_array_equal(to_np(g[n]), a, err_msg=f"int8 pool build: {n} differs")
+    return dict(k_cache=kc, v_cache=vc, k_scale=ks, v_scale=vs), g
+
+
+def run_decode(w, seed, stream, partition_size=0, n_threads=NTHREADS):
+    inp = wl.numpy_inputs(w, seed)
+    cfg = config_for(w, partition_size=partition_size)
+    if w.kv_dtype == 2:
+        host, g = build_int8_caches(w, inp, stream)
+        kc, vc, ks, vs = g["kc"], g["vc"], g["ks"], g["vs"]
+    else:
+        host = dict(k_cache=inp["k_cache"], v_cache=inp["v_cache"], k_scale=None, v_scale=None)
+        kc, vc, ks, vs = to_gpu(inp["k_cache"]), to_gpu(inp["v_cache"]), None, None
+    ref = orc.paged_decode(cfg, inp["q"], host["k_cache"], host["v_cache"], host["k_scale"],
+                           host["v_scale"], w.block_tables, w.context_lens, n_threads=n_threads)
+    S = w.num_seqs
+    out = empty_gpu((S, w.num_q_heads, w.head_dim), np.float32)
+    out.fill_(float("nan"))
+    mcl = w.max_context_len
+    wsb = pa.decode_workspace_size(cfg, S, mcl)
+    ws = empty_gpu((max(wsb, 1),), np.uint8)
+    pa.paged_decode(stream, cfg, out, to_gpu(inp["q"]), kc, vc, ks, vs, to_gpu(w.block_tables),
+                    to_gpu(w.context_lens), S, w.max_blocks, mcl, ws, wsb)
+    _sync()
+    return to_np(out), ref
+
+
+# ---- slot mapping ----------------------------------------------------------------------------------
+def test_slot_mapping_bit_exact(stream):
+    rng = np.random.default_rng(11)
+    S, mb = 37, 20
+    tables = rng.integers(0, 500, size=(S, mb)).astype(np.int32)
+    tables[rng.random((S, mb)) < 0.1] = -1
+    start = rng.integers(0, mb * 16, size=S).astype(np.int32)
+    num_new = rng.integers(0, 40, size=S).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(num_new)[:-1]]).astype(np.int32)
+    cfg = pa.make_config(num_q_heads=8, num_kv_heads=8, head_dim=64, kv_dtype=1, num_blocks=500)
+    ref = orc.build_slot_mapping(cfg, tables, start, num_new, offs)
+    out = empty_gpu((int(num_new.sum()),), np.int64)
+    pa.build_slot_mapping(stream, cfg, to_gpu(tables), mb, to_gpu(start), to_gpu(num_new), to_gpu(offs),
+                          S, int(num_new.max()), out)
+    _sync()
+    np.testing.assert_array_equal(to_np(out), ref)
+    assert (ref == -1).any() and (ref >= 0).any()
+
+
+# ---- append -----------------------------------------------------------------------------------------
+@pytest.mark.parametrize("kv_dtype,q_dtype,D", [(1, 0, 128), (0, 1, 64), (1, 1, 256), (0, 0, 128)])
+def test_append_plain_bit_exact(stream, kv_dtype, q_dtype, D):
+    rng = np.random.default_rng(20 + D + kv_dtype)
+    nb, hkv, n = 40, 4, 300
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=kv_dtype,
+                         q_dtype=q_dtype, num_blocks=nb)
+    slots = rng.permutation(nb * 16)[:n].astype(np.int64)
+    slots[::17] = -1
+    slots[5] = nb * 16 + 3  # beyond the pool: skipped
+    src_k = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    src_v = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    if q_dtype == 1:
+        src_k, src_v = orc.bf16_from_f32(src_k), orc.bf16_from_f32(src_v)
+    cdt = np.uint16 if kv_dtype == 1 else np.float32
+    init = rng.standard_normal((nb, hkv, 16, D), dtype=np.float32)
+    kc = orc.bf16_from_f32(init) if kv_dtype == 1 else init.copy()
+    vc = kc.copy()
+    gk, gv = to_gpu(kc), to_gpu(vc)
+    orc.kv_append(cfg, src_k, src_v, slots, kc, vc)
+    pa.kv_append(stream, cfg, to_gpu(src_k), to_gpu(src_v), to_gpu(slots), n, gk, gv)
+    _sync()
+    np.testing.assert_array_equal(to_np(gk, cdt), kc)
+    np.testing.assert_array_equal(to_np(gv, cdt), vc)
+
+
+@pytest.mark.parametrize("D,q_dtype", [(128, 0), (64, 1), (256, 0)])
+def test_append_int8_bit_exact(stream, D, q_dtype):
+    """Full-block build, then a decode-style 1-token append with outliers (scale growth and
+    requantisation), then a ragged multi-token append that starts mid-block."""
+    rng = np.random.default_rng(30 + D)
+    nb, hkv = 24, 4
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=2, q_dtype=q_dtype,
+                         num_blocks=nb)
+    host = dict(kc=np.zeros((nb, hkv, 16, D), np.int8), vc=np.zeros((nb, hkv, 16, D), np.int8),
+                ks=np.zeros((nb, hkv), np.float32), vs=np.zeros((nb, hkv), np.float32),
+                ka=np.zeros((nb, hkv), np.float32), va=np.zeros((nb, hkv), np.float32))
+    dev = {n: to_gpu(a) for n, a in host.items()}
+
+    def step(slots, k, v):
+        if q_dtype == 1:
+            k, v = orc.bf16_from_f32(k), orc.bf16_from_f32(v)
+        orc.kv_append(cfg, k, v, slots, host["kc"], host["vc"], host["ks"], host["vs"], host["ka"], host["va"])
+        pa.kv_append(stream, cfg, to_gpu(k), to_gpu(v), to_gpu(slots), len(slots), dev["kc"], dev["vc"],
+                     dev["ks"], dev["vs"], dev["ka"], dev["va"])
+        _sync()
+        for n, a in host.items():
+            np.testing.assert_array_equal(to_np(dev[n]), a, err_msg=n)
+
+    # 1) 12 blocks filled to 1..16 rows
+    fill = rng.integers(1, 17, size=12)
+    slots = np.concatenate([b * 16 + np.arange(f) for b, f in enumerate(fill)]).astype(np.int64)
+    k = rng.standard_normal((len(slots), hkv, D), dtype=np.float32)
+    v = rng.standard_normal((len(slots), hkv, D), dtype=np.float32)
+    step(slots, k, v)
+    # 2) one new token per partially filled block, half of them with x8 outliers (growth)
+    open_blocks = [b for b, f in enumerate(fill) if f < 16]
+    slots = np.array([b * 16 + fill[b] for b in open_blocks], np.int64)
+    k = rng.standard_normal((len(slots), hkv, D), dtype=np.float32)
+    v = rng.standard_normal((len(slots), hkv, D), dtype=np.float32)
+    k[::2, :, 3] *= 8
+    v[1::2, :, 7] *= 8
+    step(slots, k, v)
+    # 3) a 37-token chunk starting at row 5 of block 14, then -1 padding, then a new block
+    slots = np.concatenate([14 * 16 + 5 + np.arange(11), 15 * 16 + np.arange(16), 16 * 16 + np.arange(10),
+                            [-1, -1], 20 * 16 + np.arange(3)]).astype(np.int64)
+    k = rng.standard_normal((len(slots), hkv, D), dtype=np.float32) * 3
+    v = rng.standard_normal((len(slots), hkv, D), dtype=np.float32) * 3
+    step(slots, k, v)
+
+
+# ---- decode -----------------------------------------------------------------------------------------
+def test_decode_c1_fp32(stream):
+    w = wl.make_c1()
+    got, ref = run_decode(w, 101, stream)
+    check_close(got, ref, **tol_for(0), what="C1")
+
+
+def test_decode_c2_bf16_full(stream):
+    w = wl.make_c2()
+    got, ref = run_decode(w, 102, stream)
+    check_close(got, ref, **tol_for(1), what="C2")
+
+
+def test_decode_c4_int8_subset(stream):
+    w = wl.make_c4(batch=24)
+    got, ref = run_decode(w, 104, stream)
+    check_close(got, ref, **tol_for(2), what="C4 subset")
+
+
+EDGE_LENS = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 1023, 1024, 1025, 3000]
+
+
+@pytest.mark.parametrize("part", [256, 512])
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [
+    (1, 1, 32, 8, 128), (1, 0, 16, 8, 64), (1, 1, 16, 2, 256), (0, 0, 8, 2, 128), (2, 0, 8, 8, 64),
+    (2, 1, 32, 8, 128), (0, 1, 4, 4, 256),
+])
+def test_decode_edge_lengths(stream, part, kv_dtype, q_dtype, Hq, Hkv, D):
+    w = wl.make_small(7 + D + kv_dtype, num_seqs=len(EDGE_LENS), lens=EDGE_LENS, Hq=Hq, Hkv=Hkv, D=D,
+                      kv_dtype=kv_dtype, q_dtype=q_dtype)
+    got, ref = run_decode(w, 55, stream, partition_size=part)
+    check_close(got, ref, **tol_for(kv_dtype), what=f"edge lens kv={kv_dtype} D={D} G={Hq // Hkv}")
+    assert np.all(got[0] == 0.0)  # context_len 0 -> zeros
+
+
+def test_decode_invalid_block_ids_read_as_zero(stream):
+    w = wl.make_small(9, num_seqs=4, lens=[40, 300, 700, 33], Hq=16, Hkv=4, D=128, kv_dtype=1, q_dtype=1)
+    w.block_tables[1, 3] = -1
+    w.block_tables[2, 10] = w.num_blocks + 5
+    got, ref = run_decode(w, 56, stream)
+    check_close(got, ref, **tol_for(1), what="invalid ids")
