@@ -67,9 +67,12 @@ typedef enum pa_phase { PA_PHASE_PREFILL = 0, PA_PHASE_DECODE = 1 } pa_phase;
 #define PA_FLAG_NO_MASK 2u
 
 /* Shape/dtype record passed by pointer to every launch function.
- * KV cache layout (per layer, K and V separately): [num_blocks][num_kv_heads][block_size][head_dim]
- * of kv_dtype -- the reference's intended per-block tensor [layers, heads, blockSize, headDim]
- * (src/MLFramework/Inference/PagedAttention/Layers/PagedAttentionLayer.cs:315) for one layer.
+ * KV cache layout (per layer, K and V in separate buffers of kv_dtype), one tile per
+ * (block, KV head) as in the reference's intended per-block tensor [layers, heads, blockSize,
+ * headDim] (src/MLFramework/Inference/PagedAttention/Layers/PagedAttentionLayer.cs:315):
+ *   K: [num_blocks][num_kv_heads][block_size][head_dim]   (token rows, row-major)
+ *   V: [num_blocks][num_kv_heads][head_dim][block_size]   (dim rows: the tile is transposed so
+ *      that P.V reads the 16 tokens of one dimension as one contiguous run)
  * int8 scales and running absolute maxima: fp32 [num_blocks][num_kv_heads], K and V separately. */
 typedef struct pa_config {
     int32_t block_size;     /* tokens per physical block; 16 in every shipped configuration    */
@@ -79,7 +82,8 @@ typedef struct pa_config {
     int32_t kv_dtype;       /* pa_dtype of the cache                                            */
     int32_t q_dtype;        /* pa_dtype of Q and of the new K/V handed to pa_kv_append (FP32/BF16) */
     int32_t num_blocks;     /* physical blocks in the pool; ids outside [0, num_blocks) are
-                               never dereferenced (their tokens are skipped)                    */
+                               never dereferenced (decode/prefill read their tokens as zeros,
+                               append skips their slots)                                        */
     float   scale;          /* softmax scale; <= 0 selects 1/sqrtf(head_dim)
                                (StandardPagedAttentionKernel.cs:18,28)                          */
     int32_t partition_size; /* decode split-K partition length in tokens; 0 = library default  */
@@ -193,7 +197,8 @@ pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs,
  *   q:   [num_seqs][num_q_heads][head_dim] of cfg->q_dtype
  *   block_tables: [num_seqs][max_blocks_per_seq] int32, context_lens: [num_seqs] int32
  *   max_context_len: host-side upper bound of context_lens (sizes the grid); tokens beyond it,
- *   or beyond max_blocks_per_seq * block_size, are not read.
+ *   or beyond max_blocks_per_seq * block_size, are not read. Tokens whose table entry lies
+ *   outside [0, num_blocks) read as zero keys and values (never dereferenced).
  * Sequences longer than one partition (cfg->partition_size) are split across workgroups and
  * merged with a log-sum-exp reduction through `workspace`. A sequence with context_len <= 0
  * produces zeros. */

@@ -51,7 +51,9 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         const int h = idx / head_dim, d = idx - h * head_dim;
         const float x = load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
-        const int64_t o = ((blk * num_kv_heads + h) * pa::kBlockSize + off) * head_dim + d;
+        const int64_t tile = (blk * num_kv_heads + h) * pa::kBlockSize * head_dim;
+        // K tiles are [16][D] (token rows); V tiles are [D][16] (dim rows).
+        const int64_t o = blockIdx.y == 0 ? tile + off * head_dim + d : tile + static_cast<int64_t>(d) * pa::kBlockSize + off;
         if (cache_bf16) static_cast<uint16_t*>(dst)[o] = pa::bf16_trunc(x);
         else static_cast<float*>(dst)[o] = x;
     }
@@ -105,6 +107,10 @@ __global__ __launch_bounds__(64) void append_int8_kernel(
 
     const int64_t sidx = blk * num_kv_heads + h;
     int8_t* block_codes = cache + ((blk * num_kv_heads + h) * pa::kBlockSize) * D;
+    // Element (row off, dim d) of the tile: K is [16][D], V is [D][16].
+    auto at = [&](int off, int d) -> int8_t* {
+        return is_v ? block_codes + d * pa::kBlockSize + off : block_codes + off * D + d;
+    };
     float cur_scale;
     if (fresh) {
         // Writing row 0 starts the block: earlier contents and statistics are discarded.
@@ -125,7 +131,7 @@ __global__ __launch_bounds__(64) void append_int8_kernel(
                 if (written & (1u << off)) continue;
 #pragma unroll
                 for (int k = 0; k < kPer; k++) {
-                    int8_t* c = block_codes + off * D + lane + 64 * k;
+                    int8_t* c = at(off, lane + 64 * k);
                     const float deq = static_cast<float>(static_cast<int32_t>(*c)) * old_scale;
                     *c = pa::quantize_symmetric(deq, cur_scale);
                 }
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(64) void append_int8_kernel(
 #pragma unroll
         for (int k = 0; k < kPer; k++) {
             const float x = load_act(src, in_bf16, base + lane + 64 * k);
-            block_codes[off * D + lane + 64 * k] = pa::quantize_symmetric(x, cur_scale);
+            *at(off, lane + 64 * k) = pa::quantize_symmetric(x, cur_scale);
         }
     }
 }

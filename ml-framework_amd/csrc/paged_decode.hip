@@ -5,47 +5,31 @@
 // which gathers each sequence's K/V and calls StandardPagedAttentionKernel once per sequence,
 // Kernels/StandardPagedAttentionKernel.cs:21-84) with one launch over the whole ragged batch.
 //
-// Work decomposition: one workgroup (256 threads = 4 waves) per (partition, KV head, sequence).
-// A partition is PART consecutive tokens (PART / 16 blocks) of one sequence; sequences that fit in
-// one partition are finished in place, longer ones write per-partition (max, sum, unnormalised
-// output) to the workspace and a second kernel merges them with a log-sum-exp reduction.
+// Work decomposition: one workgroup (4 waves) per (partition, KV head, sequence). A partition is a
+// run of `part` tokens (whole 16-token blocks) of one sequence. A sequence that fits in one
+// partition is finished in place; longer ones write per-partition (max, sum, unnormalised output)
+// to the workspace and paged_decode_merge_kernel combines them with a log-sum-exp reduction.
 // The G = Hq / Hkv query heads of a KV head share every K/V byte loaded (GQA).
 //
-// Per wave and 16-token block, each lane loads 16-byte chunks: lane = (token-in-group ti, chunk ch),
-// CH = D * elt / 16 chunks per token row, TPI = 64 / CH tokens per load instruction, so every load
-// instruction of a wave reads 1 KiB of contiguous cache. q.k partial dots are summed across the CH
-// lanes of a token with DPP; scores go to LDS, the partition's softmax statistics are block-reduced,
-// and P.V accumulates per lane in fp32, reduced across token groups and waves at the end.
+// bf16 / int8 caches (paged_decode_mfma_kernel): each wave streams its blocks (every 4th block of
+// the partition) with a one-block prefetch. Per block, S^T[16 tokens][16 heads] = K . Q^T runs on
+// v_mfma_f32_16x16x32_bf16 (query heads padded to 16 rows) and O[16 heads][D] += P . V on
+// v_mfma_f32_16x16x16_bf16 with P split into bf16 high and low parts, so the probabilities keep
+// ~16 bits. The score layout the first MFMA leaves in registers (lane = (token group, head)) is
+// exactly the A-operand layout of the second, so P never leaves registers. Softmax is online per
+// wave in fp32; the four waves are combined through LDS at the end.
+// fp32 caches (paged_decode_fp32_kernel): VALU dot products reduced across lanes with DPP, a
+// partition-wide softmax in LDS, and VALU P.V.
 #include <string>
+#include <type_traits>
 
 #include "pa_internal.h"
 
 namespace {
 
-template <int KV> struct KvT;
-template <> struct KvT<PA_DTYPE_FP32> { static constexpr int kElt = 4; };
-template <> struct KvT<PA_DTYPE_BF16> { static constexpr int kElt = 2; };
-template <> struct KvT<PA_DTYPE_INT8> { static constexpr int kElt = 1; };
-
-template <int KV, int EPC>
-__device__ __forceinline__ void unpack(const uint4& r, float (&f)[EPC]) {
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-    if constexpr (KV == PA_DTYPE_FP32) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) f[k] = __uint_as_float(w[k]);
-    } else if constexpr (KV == PA_DTYPE_BF16) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            f[2 * k] = pa::bf16_lo(w[k]);
-            f[2 * k + 1] = pa::bf16_hi(w[k]);
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) f[4 * k + b] = pa::i8_at(w[k], b);
-    }
-}
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct DecodeArgs {
     float* out;
@@ -60,10 +44,12 @@ struct DecodeArgs {
     float* ws_m;  // [num_seqs][Hq][max_parts]
     float* ws_l;  // [num_seqs][Hq][max_parts]
     int32_t num_kv_heads;
+    int32_t group;  // G = Hq / Hkv
     int32_t max_blocks_per_seq;
     int32_t num_blocks;
     int32_t max_context_len;
     int32_t max_parts;
+    int32_t part;  // partition length in tokens (multiple of 64)
     int32_t q_bf16;
     float scale;
 };
@@ -75,22 +61,419 @@ __device__ __forceinline__ int clamp_len(const DecodeArgs& a, int seq) {
     return T;
 }
 
-template <int D, int KV, int G, int PART>
-__global__ __launch_bounds__(256) void paged_decode_kernel(const DecodeArgs a) {
-    constexpr int ELT = KvT<KV>::kElt;
-    constexpr int CH = D * ELT / 16;  // 16-byte chunks per token row
-    constexpr int EPC = 16 / ELT;     // elements per chunk
-    constexpr int TPI = 64 / CH;      // tokens per wave load instruction
-    constexpr int LPB = 16 / TPI;     // load instructions per block per lane
-    constexpr int NBP = PART / 16;    // blocks per partition
-    constexpr int NBW = NBP / 4;      // blocks per wave
-    constexpr int TPT = PART / 256;   // softmax tokens per thread
-    // Loads are hoisted ahead of the math while they fit in registers (bytes in flight hide HBM
-    // latency); wider rows (fp32 D >= 128, D = 256) load block by block instead.
-    constexpr bool kPreloadK = NBW * LPB <= 32;
-    constexpr bool kPreloadV = NBW * LPB <= 16;
-    static_assert(CH >= 4 && CH <= 64, "unsupported head_dim / dtype combination");
-    static_assert(PART % 256 == 0, "PART must be a multiple of 256");
+// Final write of one (sequence, query head, dim): normalised output, or the partition's partial.
+__device__ __forceinline__ void emit(const DecodeArgs& a, int seq, int h, int part, int nparts, int D,
+                                     int d, float o, float m, float l) {
+    const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * a.group + h;
+    if (nparts == 1) {
+        a.out[row * D + d] = o / l;
+    } else {
+        const int64_t pidx = row * a.max_parts + part;
+        a.ws_o[pidx * D + d] = o;
+        if (d == 0) {
+            a.ws_m[pidx] = m;
+            a.ws_l[pidx] = l;
+        }
+    }
+}
+
+// ================================================================================================
+// bf16 / int8 caches: MFMA kernel.
+// ================================================================================================
+template <int KV> struct MfmaRaw;
+template <> struct MfmaRaw<PA_DTYPE_BF16> {
+    using K = uint4;  // 8 bf16 of one token row (A operand of the 16x16x32 MFMA)
+    using V = uint2;  // 4 bf16: 4 consecutive tokens of one dim (B operand of the 16x16x16 MFMA)
+    static constexpr int kElt = 2;
+};
+template <> struct MfmaRaw<PA_DTYPE_INT8> {
+    using K = uint2;     // 8 int8 codes
+    using V = uint32_t;  // 4 int8 codes
+    static constexpr int kElt = 1;
+};
+
+// fp32 -> bf16 bits by truncation (the reference's conversion, BFloat16.cs:99-107).
+__device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
+    return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_i8pair(uint32_t w, int k) {
+    // Codes k and k+1 of w as two bf16 (exact: |code| <= 128 needs 8 significant bits).
+    return pack_bf16_trunc(pa::i8_at(w, k), pa::i8_at(w, k + 1));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ bf16x8_t k_operand(const uint4& r) { return __builtin_bit_cast(bf16x8_t, r); }
+__device__ __forceinline__ bf16x8_t k_operand(const uint2& r) {
+    const uint4 p = make_uint4(pack_i8pair(r.x, 0), pack_i8pair(r.x, 2), pack_i8pair(r.y, 0), pack_i8pair(r.y, 2));
+    return __builtin_bit_cast(bf16x8_t, p);
+}
+__device__ __forceinline__ s16x4_t v_operand(const uint2& r) { return __builtin_bit_cast(s16x4_t, r); }
+__device__ __forceinline__ s16x4_t v_operand(const uint32_t& r) {
+    const uint2 p = make_uint2(pack_i8pair(r, 0), pack_i8pair(r, 2));
+    return __builtin_bit_cast(s16x4_t, p);
+}
+
+// Online-softmax rescaling is deferred until a block's max exceeds the running max by more than
+// this (natural-log units): probabilities then stay below e^8 and fp32 sums stay exact enough,
+// while the O accumulators are rescaled on few blocks instead of on most of them.
+constexpr float kRescaleThreshold = 8.0f;
+constexpr int kMaxPersistentSeqs = 4096;  // sequence-prefix table held in LDS
+
+struct MfmaShared {
+    float m[4][16];
+    float l[4][16];
+    int pref[kMaxPersistentSeqs + 1];  // items before sequence s (persistent mode)
+};
+
+// One work item: (sequence, KV head, partition). Called by all 256 threads of a workgroup.
+template <int D, int KV, bool QF32>
+__device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh, int part, MfmaShared& sh,
+                                          float (*s_x)[D][16]) {
+    using Raw = MfmaRaw<KV>;
+    constexpr int ELT = Raw::kElt;
+    constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
+    constexpr int NT = D / 16;     // PV n-tiles of 16 dims
+    constexpr int TILE = 16 * D;   // elements per (block, KV head) tile
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q4 = lane >> 4;  // token group (QK C rows) / k group of the MFMA operands
+    const int n = lane & 15;   // head column of S^T / row of P / dim within a PV tile
+    const int G = a.group, Hkv = a.num_kv_heads;
+
+    const int T = clamp_len(a, seq);
+    const int tok0 = part * a.part;
+    if (T <= 0) {
+        if (part == 0)
+            for (int idx = tid; idx < G * D; idx += 256)
+                a.out[(static_cast<int64_t>(seq) * Hkv * G + kvh * G) * D + idx] = 0.0f;
+        return;
+    }
+    if (tok0 >= T) return;
+    const int tok_end = min(T, tok0 + a.part);
+    const int nparts = (T + a.part - 1) / a.part;
+
+    // This wave's blocks: lb0 + wave + 4j, j < nb. Lane j holds block j's id (and int8 scales).
+    const int lb0 = tok0 / 16;
+    const int nblk = (tok_end - tok0 + 15) / 16;
+    const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;
+    const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
+    int my_bid = -1;
+    float my_ks = 0.0f, my_vs = 0.0f;
+    if (lane < nb) {
+        my_bid = table[lb0 + wave + 4 * lane];
+        if (my_bid >= a.num_blocks) my_bid = -1;
+        if constexpr (KV == PA_DTYPE_INT8) {
+            if (my_bid >= 0) {
+                my_ks = a.k_scale[static_cast<int64_t>(my_bid) * Hkv + kvh];
+                my_vs = a.v_scale[static_cast<int64_t>(my_bid) * Hkv + kvh];
+            }
+        }
+    }
+
+    // Q^T operand: lane (q4, n) holds head n, dims 32s + 8q4 .. +8 (zero rows for n >= G).
+    bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
+    {
+        const bool hv = n < G;
+        const int64_t qrow = (static_cast<int64_t>(seq) * Hkv * G + kvh * G + (hv ? n : 0)) * D;
+#pragma unroll
+        for (int s = 0; s < NSLAB; s++) {
+            const int d0 = 32 * s + 8 * q4;
+            if constexpr (QF32) {
+                const float* qp = static_cast<const float*>(a.q) + qrow + d0;
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = hv ? qp[e] : 0.0f;
+                uint32_t h[4], l[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    h[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
+                    const float r0 = x[2 * e] - __uint_as_float(__float_as_uint(x[2 * e]) & 0xffff0000u);
+                    const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
+                    l[e] = pack_bf16_trunc(r0, r1);
+                }
+                qhi[s] = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+                qlo[s] = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+            } else {
+                const uint4 raw = hv ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
+                                     : make_uint4(0, 0, 0, 0);
+                qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
+            }
+        }
+    }
+
+    const char* kc = static_cast<const char*>(a.k_cache);
+    const char* vc = static_cast<const char*>(a.v_cache);
+    using KR = typename Raw::K;
+    using VR = typename Raw::V;
+    auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
+        const int bid = __builtin_amdgcn_readlane(my_bid, j);
+        if (bid >= 0) {
+            const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * TILE;
+            const char* kt = kc + (tile + n * D + 8 * q4) * ELT;
+            const char* vt = vc + (tile + n * 16 + 4 * q4) * ELT;
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) kr[s] = *reinterpret_cast<const KR*>(kt + 32 * s * ELT);
+#pragma unroll
+            for (int t = 0; t < NT; t++) vr[t] = *reinterpret_cast<const VR*>(vt + 256 * t * ELT);
+        } else {
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) kr[s] = KR{};
+#pragma unroll
+            for (int t = 0; t < NT; t++) vr[t] = VR{};
+        }
+    };
+
+    float m_run = -INFINITY;  // reference max of head n (exceeded by at most kRescaleThreshold)
+    float l_run = 0.0f;       // this lane's share of the running sum of head n
+    f32x4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], int j) {
+        // S^T[token 4q4+i][head n]
+        f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++) {
+            const bf16x8_t kop = k_operand(kr[sl]);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
+            if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+        }
+        float ks = 1.0f, vfac = 1.0f;
+        if constexpr (KV == PA_DTYPE_INT8) {
+            ks = readlane_f(my_ks, j);
+            vfac = readlane_f(my_vs, j);
+        }
+        const int tbase = (lb0 + wave + 4 * j) * 16 + 4 * q4;
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v = s[i];
+            if constexpr (KV == PA_DTYPE_INT8) v = v * ks;  // (q . code) * k_scale, then * scale
+            v = v * a.scale;
+            sc[i] = tbase + i < T ? v : -INFINITY;
+        }
+        float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const bool grow = bm > m_run + kRescaleThreshold;
+        if (__any(grow)) {
+            const float m_new = grow ? bm : m_run;
+            const float alpha = __expf(m_run - m_new);  // 1 where the max did not move, 0 from -inf
+            l_run *= alpha;
+            m_run = m_new;
+            float ar[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][i] *= ar[i];
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p[i] = __expf(sc[i] - m_run);
+            l_run += p[i];
+            if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
+        }
+        uint32_t hi[2], lo[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float a0 = p[2 * e], a1 = p[2 * e + 1];
+            const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+            const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+            hi[e] = pack_bf16_trunc(a0, a1);
+            lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+        }
+        const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+        const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const s16x4_t vop = v_operand(vr[t]);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+        }
+    };
+
+    {
+        // Three rotating register buffers: two blocks in flight while a third is consumed.
+        KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
+        VR va[NT], vb[NT], vx[NT];
+        int j = 0;
+        if (nb > 0) load(ka, va, 0);
+        if (nb > 1) load(kb, vb, 1);
+        while (j < nb) {
+            if (j + 2 < nb) load(kx, vx, j + 2);
+            compute(ka, va, j);
+            if (++j >= nb) break;
+            if (j + 2 < nb) load(ka, va, j + 2);
+            compute(kb, vb, j);
+            if (++j >= nb) break;
+            if (j + 2 < nb) load(kb, vb, j + 2);
+            compute(kx, vx, j);
+            ++j;
+        }
+    }
+
+    // ---- combine the 4 waves: weights exp(m_w - M) per head, then a 2-level tree in LDS ----
+    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    if (q4 == 0) {
+        sh.m[wave][n] = m_run;
+        sh.l[wave][n] = l_tot;
+    }
+    __syncthreads();
+    float M[4], f_own[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int h = 4 * q4 + i;
+        M[i] = fmaxf(fmaxf(sh.m[0][h], sh.m[1][h]), fmaxf(sh.m[2][h], sh.m[3][h]));
+        f_own[i] = __expf(sh.m[wave][h] - M[i]);  // 0 for a wave that saw no block
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[t][i] *= f_own[i];
+    // acc[t] holds rows 4q4..4q4+3 of dim 16t+n: one 16-byte LDS store in the [dim][row] layout.
+    if (wave >= 2) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) *reinterpret_cast<f32x4_t*>(&s_x[wave - 2][16 * t + n][4 * q4]) = acc[t];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            f32x4_t* slot = reinterpret_cast<f32x4_t*>(&s_x[wave][16 * t + n][4 * q4]);
+            acc[t] += *slot;
+            if (wave == 1) *slot = acc[t];
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float L[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * q4 + i;
+            L[i] = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) L[i] += sh.l[w][h] * __expf(sh.m[w][h] - M[i]);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const f32x4_t other = *reinterpret_cast<const f32x4_t*>(&s_x[1][16 * t + n][4 * q4]);
+            acc[t] += other;
+        }
+        if (4 * q4 < G) {
+            const int64_t row0 = static_cast<int64_t>(seq) * Hkv * G + kvh * G;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * q4 + i;
+                if (h >= G) break;
+                const int64_t row = row0 + h;
+                if (nparts == 1) {
+                    const float inv = 1.0f / L[i];
+#pragma unroll
+                    for (int t = 0; t < NT; t++) a.out[row * D + 16 * t + n] = acc[t][i] * inv;
+                } else {
+                    const int64_t pidx = row * a.max_parts + part;
+#pragma unroll
+                    for (int t = 0; t < NT; t++) a.ws_o[pidx * D + 16 * t + n] = acc[t][i];
+                    if (n == 0) {
+                        a.ws_m[pidx] = M[i];
+                        a.ws_l[pidx] = L[i];
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();  // LDS reuse by the next item
+}
+
+// Grid mode: one workgroup per (partition, KV head, sequence).
+template <int D, int KV, bool QF32>
+__global__ __launch_bounds__(256, 2) void paged_decode_mfma_kernel(const DecodeArgs a) {
+    __shared__ MfmaShared sh;
+    __shared__ float s_x[2][D][16];
+    mfma_item<D, KV, QF32>(a, blockIdx.z, blockIdx.y, blockIdx.x, sh, s_x);
+}
+
+// Persistent mode: gridDim.x workgroups walk the compacted list of non-empty items
+// (sequence s owns items pref[s]*Hkv .. pref[s+1]*Hkv - 1, KV head fastest), item w, w + grid, ...
+// Every workgroup leaves its loop after a bounded number of items.
+template <int D, int KV, bool QF32>
+__global__ __launch_bounds__(256, 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a, int32_t num_seqs) {
+    __shared__ MfmaShared sh;
+    __shared__ float s_x[2][D][16];
+    const int tid = threadIdx.x;
+    // Items per sequence: its partition count (a zero-length sequence still gets one item, which
+    // writes its zero output). Exclusive prefix over sequences, built by the whole workgroup.
+    constexpr int PER = (kMaxPersistentSeqs + 255) / 256;
+    int cnt[PER];
+    int local = 0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int s = tid * PER + k;
+        int c = 0;
+        if (s < num_seqs) {
+            const int T = clamp_len(a, s);
+            c = T <= 0 ? 1 : (T + a.part - 1) / a.part;
+        }
+        cnt[k] = c;
+        local += c;
+    }
+    // block-wide exclusive scan of `local`
+    const int lane = tid & 63, wave = tid >> 6;
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) sh.pref[wave] = incl;  // wave totals (scratch, overwritten below)
+    __syncthreads();
+    int wave_off = 0;
+    for (int w = 0; w < wave; w++) wave_off += sh.pref[w];
+    const int total_parts = sh.pref[0] + sh.pref[1] + sh.pref[2] + sh.pref[3];
+    __syncthreads();
+    int run = wave_off + incl - local;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int s = tid * PER + k;
+        if (s <= num_seqs) sh.pref[s] = run;
+        run += cnt[k];
+    }
+    __syncthreads();
+
+    const int Hkv = a.num_kv_heads;
+    const int64_t total = static_cast<int64_t>(total_parts) * Hkv;
+    int seq = 0;
+    for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+        const int pi = static_cast<int>(item / Hkv);
+        const int kvh = static_cast<int>(item - static_cast<int64_t>(pi) * Hkv);
+        // Items only increase, so the owning sequence is found by scanning forward.
+        while (seq + 1 < num_seqs && sh.pref[seq + 1] <= pi) seq++;
+        mfma_item<D, KV, QF32>(a, seq, kvh, pi - sh.pref[seq], sh, s_x);
+    }
+}
+
+// ================================================================================================
+// fp32 caches: VALU kernel.
+// ================================================================================================
+template <int D, int G, int PART>
+__global__ __launch_bounds__(256) void paged_decode_fp32_kernel(const DecodeArgs a) {
+    constexpr int CH = D / 4;      // 16-byte chunks per K row
+    constexpr int TPI = 64 / CH;   // K rows per wave load instruction
+    constexpr int LPB = 16 / TPI;  // K load instructions per block per lane
+    constexpr int RPL = D / 16;    // V dim rows per lane per block (lane = (dim row, 4-token chunk))
+    constexpr int NBW = PART / 64; // blocks per wave
+    constexpr int TPT = PART / 256;
+    constexpr int TILE = 16 * D;
+    static_assert(CH >= 16 && CH <= 64, "fp32 kernel covers head_dim 64..256");
 
     __shared__ float s_logits[G][PART];
     __shared__ float s_red[4][G];
@@ -114,19 +497,17 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(const DecodeArgs a) {
     const int nparts = (T + PART - 1) / PART;
     const int ti = lane / CH, ch = lane % CH;
 
-    // This lane's slice of the G query heads.
-    float qf[G][EPC];
+    float qf[G][4];
     {
-        const int64_t qb = (static_cast<int64_t>(seq) * Hq + kvh * G) * D + ch * EPC;
+        const int64_t qb = (static_cast<int64_t>(seq) * Hq + kvh * G) * D + ch * 4;
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < EPC; e++)
+            for (int e = 0; e < 4; e++)
                 qf[g][e] = a.q_bf16 ? pa::bf16_to_f32(static_cast<const uint16_t*>(a.q)[qb + g * D + e])
                                     : static_cast<const float*>(a.q)[qb + g * D + e];
     }
 
-    // Physical block ids of this wave's blocks (wave-uniform).
     const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
     const int lb0 = tok0 / 16;
     int bid[NBW];
@@ -140,60 +521,41 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(const DecodeArgs a) {
         }
         bid[i] = __builtin_amdgcn_readfirstlane(id);
     }
-
-    const char* kc = static_cast<const char*>(a.k_cache);
-    const char* vc = static_cast<const char*>(a.v_cache);
-    auto chunk_off = [&](int b, int j) -> int64_t {
-        return ((static_cast<int64_t>(b) * Hkv + kvh) * 16 + j * TPI + ti) * (D * ELT) + ch * 16;
+    const float* kc = static_cast<const float*>(a.k_cache);
+    const float* vc = static_cast<const float*>(a.v_cache);
+    auto kload = [&](int b, int j) -> uint4 {
+        if (b < 0) return make_uint4(0, 0, 0, 0);
+        return *reinterpret_cast<const uint4*>(kc + (static_cast<int64_t>(b) * Hkv + kvh) * TILE +
+                                               (j * TPI + ti) * D + ch * 4);
     };
 
-    auto load = [&](const char* base, int b, int j) -> uint4 {
-        return b >= 0 ? *reinterpret_cast<const uint4*>(base + chunk_off(b, j)) : make_uint4(0, 0, 0, 0);
-    };
-    uint4 kr[kPreloadK ? NBW : 1][LPB];
-    uint4 vr[kPreloadV ? NBW : 1][LPB];
-#pragma unroll
-    for (int i = 0; i < NBW; i++)
-#pragma unroll
-        for (int j = 0; j < LPB; j++) {
-            if constexpr (kPreloadK) kr[i][j] = load(kc, bid[i], j);
-            if constexpr (kPreloadV) vr[i][j] = load(vc, bid[i], j);
-        }
-
-    // ---- scores: s = (q . k) * scale  (int8: (q . k_code) * k_scale * scale) ----
+    // ---- scores ----
 #pragma unroll
     for (int i = 0; i < NBW; i++) {
-        float ks = 1.0f;
-        if constexpr (KV == PA_DTYPE_INT8) ks = bid[i] >= 0 ? a.k_scale[static_cast<int64_t>(bid[i]) * Hkv + kvh] : 0.0f;
+        uint4 kr[LPB];
+#pragma unroll
+        for (int j = 0; j < LPB; j++) kr[j] = kload(bid[i], j);
 #pragma unroll
         for (int j = 0; j < LPB; j++) {
-            uint4 raw;
-            if constexpr (kPreloadK) raw = kr[i][j];
-            else raw = load(kc, bid[i], j);
-            float kf[EPC];
-            unpack<KV, EPC>(raw, kf);
+            const float kf[4] = {__uint_as_float(kr[j].x), __uint_as_float(kr[j].y), __uint_as_float(kr[j].z),
+                                 __uint_as_float(kr[j].w)};
             float dot[G];
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 float acc = 0.0f;
 #pragma unroll
-                for (int e = 0; e < EPC; e++) acc += qf[g][e] * kf[e];
+                for (int e = 0; e < 4; e++) acc += qf[g][e] * kf[e];
                 dot[g] = pa::group_sum<CH>(acc);
             }
             const int lt = (i * 4 + wave) * 16 + j * TPI + ti;
-            if (ch == 0) {
+            if (ch == 0)
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float sc = dot[g];
-                    if constexpr (KV == PA_DTYPE_INT8) sc = sc * ks;
-                    s_logits[g][lt] = lt < ntok ? sc * a.scale : -INFINITY;
-                }
-            }
+                for (int g = 0; g < G; g++) s_logits[g][lt] = lt < ntok ? dot[g] * a.scale : -INFINITY;
         }
     }
     __syncthreads();
 
-    // ---- partition softmax statistics: m = max s, p = exp(s - m), l = sum p ----
+    // ---- partition softmax ----
     float m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -223,123 +585,216 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int g = 0; g < G; g++) l[g] = (s_red[0][g] + s_red[1][g]) + (s_red[2][g] + s_red[3][g]);
 
-    // ---- o = sum_t p_t * v_t ----
-    float acc[G][EPC];
+    // ---- o = sum_t p_t v_t; V tile is [D][16]: lane = (dim row vd + 16 r, tokens 4vc..4vc+3) ----
+    const int vc4 = lane & 3, vd = lane >> 2;
+    float acc[G][RPL];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < EPC; e++) acc[g][e] = 0.0f;
+        for (int r = 0; r < RPL; r++) acc[g][r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NBW; i++) {
-        float vs = 1.0f;
-        if constexpr (KV == PA_DTYPE_INT8) vs = bid[i] >= 0 ? a.v_scale[static_cast<int64_t>(bid[i]) * Hkv + kvh] : 0.0f;
+        if (bid[i] < 0) continue;  // zero values contribute nothing
+        const float* vt = vc + (static_cast<int64_t>(bid[i]) * Hkv + kvh) * TILE + vd * 16 + 4 * vc4;
+        uint4 vr[RPL];
 #pragma unroll
-        for (int j = 0; j < LPB; j++) {
-            uint4 raw;
-            if constexpr (kPreloadV) raw = vr[i][j];
-            else raw = load(vc, bid[i], j);
-            float vf[EPC];
-            unpack<KV, EPC>(raw, vf);
-            const int lt = (i * 4 + wave) * 16 + j * TPI + ti;
+        for (int r = 0; r < RPL; r++) vr[r] = *reinterpret_cast<const uint4*>(vt + r * 256);
+        const int lt = (i * 4 + wave) * 16 + 4 * vc4;
+        float4 p[G];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                float p = s_logits[g][lt];
-                if constexpr (KV == PA_DTYPE_INT8) p = p * vs;
+        for (int g = 0; g < G; g++) p[g] = *reinterpret_cast<const float4*>(&s_logits[g][lt]);
 #pragma unroll
-                for (int e = 0; e < EPC; e++) acc[g][e] += p * vf[e];
-            }
+        for (int r = 0; r < RPL; r++) {
+            const float v0 = __uint_as_float(vr[r].x), v1 = __uint_as_float(vr[r].y);
+            const float v2 = __uint_as_float(vr[r].z), v3 = __uint_as_float(vr[r].w);
+#pragma unroll
+            for (int g = 0; g < G; g++) acc[g][r] += p[g].x * v0 + p[g].y * v1 + p[g].z * v2 + p[g].w * v3;
         }
     }
-    // Sum the TPI token groups of the wave (lanes ch, ch + CH, ...).
 #pragma unroll
-    for (int off = CH; off < 64; off <<= 1)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < EPC; e++) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
-    if (ti == 0)
+        for (int r = 0; r < RPL; r++) acc[g][r] = pa::group_sum<4>(acc[g][r]);
+    if (vc4 == 0)
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int e = 0; e < EPC; e++) s_o[wave][g][ch * EPC + e] = acc[g][e];
+            for (int r = 0; r < RPL; r++) s_o[wave][g][vd + 16 * r] = acc[g][r];
     __syncthreads();
 
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, d = idx - g * D;
         const float o = (s_o[0][g][d] + s_o[1][g][d]) + (s_o[2][g][d] + s_o[3][g][d]);
-        const int64_t row = static_cast<int64_t>(seq) * Hq + kvh * G + g;
-        if (nparts == 1) {
-            a.out[row * D + d] = o / l[g];
-        } else {
-            const int64_t pidx = row * a.max_parts + part;
-            a.ws_o[pidx * D + d] = o;
-            if (d == 0) {
-                a.ws_m[pidx] = m[g];
-                a.ws_l[pidx] = l[g];
-            }
-        }
+        emit(a, seq, kvh * G + g, part, nparts, D, d, o, m[g], l[g]);
     }
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, query head).
+// ================================================================================================
+// Log-sum-exp merge of the partitions of one (sequence, KV head): one wave per query head.
+// Partition statistics are read 64 at a time (one per lane); the weighted sum over partitions
+// issues its loads in groups of 8 so their latencies overlap.
+// ================================================================================================
 template <int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a, int32_t part_size) {
-    const int h = blockIdx.x, seq = blockIdx.y, Hq = gridDim.x;
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
+    constexpr int DPL = D / 64;  // dims per lane
+    const int kvh = blockIdx.x, seq = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = a.group;
     const int T = clamp_len(a, seq);
     if (T <= 0) return;
-    const int nparts = (T + part_size - 1) / part_size;
+    const int nparts = (T + a.part - 1) / a.part;
     if (nparts <= 1) return;
-    const int64_t row = static_cast<int64_t>(seq) * Hq + h;
-    const int64_t base = row * a.max_parts;
-    float M = -INFINITY;
-    for (int p = 0; p < nparts; p++) M = fmaxf(M, a.ws_m[base + p]);
-    float L = 0.0f;
-    for (int p = 0; p < nparts; p++) L += a.ws_l[base + p] * __expf(a.ws_m[base + p] - M);
-    const float inv = 1.0f / L;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float o = 0.0f;
-        for (int p = 0; p < nparts; p++) o += a.ws_o[(base + p) * D + d] * __expf(a.ws_m[base + p] - M);
-        a.out[row * D + d] = o * inv;
+    for (int g = wave; g < G; g += 4) {
+        const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
+        const int64_t base = row * a.max_parts;
+        float M = -INFINITY;
+        for (int p0 = 0; p0 < nparts; p0 += 64)
+            if (p0 + lane < nparts) M = fmaxf(M, a.ws_m[base + p0 + lane]);
+        M = pa::wave_max(M);
+        float L = 0.0f;
+        float o[DPL];
+#pragma unroll
+        for (int k = 0; k < DPL; k++) o[k] = 0.0f;
+        for (int p0 = 0; p0 < nparts; p0 += 64) {
+            const int cnt = min(64, nparts - p0);
+            float w = 0.0f;
+            if (lane < cnt) {
+                w = __expf(a.ws_m[base + p0 + lane] - M);
+                L += a.ws_l[base + p0 + lane] * w;
+            }
+            const float* src = a.ws_o + (base + p0) * D + lane;
+            int p = 0;
+            for (; p + 8 <= cnt; p += 8) {
+                float v[8][DPL];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int k = 0; k < DPL; k++) v[u][k] = src[(p + u) * D + 64 * k];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float wu = readlane_f(w, p + u);
+#pragma unroll
+                    for (int k = 0; k < DPL; k++) o[k] += v[u][k] * wu;
+                }
+            }
+            for (; p < cnt; p++) {
+                const float wu = readlane_f(w, p);
+#pragma unroll
+                for (int k = 0; k < DPL; k++) o[k] += src[p * D + 64 * k] * wu;
+            }
+        }
+        L = pa::wave_sum(L);
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
     }
 }
 
-constexpr int kDefaultPart = 256;
+// ---- host side ---------------------------------------------------------------------------------
+constexpr int kMaxPart = 4096;  // a wave's block ids must fit one VGPR (64 lanes x 4 waves x 16)
 
-template <int D, int KV, int G>
-void launch_decode(const DecodeArgs& a, int part, dim3 grid, hipStream_t s) {
-    if (part == 512) paged_decode_kernel<D, KV, G, 512><<<grid, 256, 0, s>>>(a);
-    else paged_decode_kernel<D, KV, G, 256><<<grid, 256, 0, s>>>(a);
-}
-
-template <int D, int KV>
-bool dispatch_g(int G, const DecodeArgs& a, int part, dim3 grid, hipStream_t s) {
-    switch (G) {
-        case 1: launch_decode<D, KV, 1>(a, part, grid, s); return true;
-        case 2: launch_decode<D, KV, 2>(a, part, grid, s); return true;
-        case 4: launch_decode<D, KV, 4>(a, part, grid, s); return true;
-        case 8: launch_decode<D, KV, 8>(a, part, grid, s); return true;
-        default: return false;
+// Partition length for this call. fp32 caches use 256 or 512 (VALU kernel templates); bf16/int8
+// take any multiple of 64 up to 4096, defaulting to about 1/16 of the longest context (at least
+// 256), which keeps the partial count per sequence at or under 16.
+int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
+    const int req = cfg->partition_size;
+    if (cfg->kv_dtype == PA_DTYPE_FP32) {
+        if (req == 0) return 256;
+        if (req == 256 || req == 512) return req;
+        *err = "partition_size must be 0, 256 or 512 for an fp32 cache";
+        return -1;
     }
-}
-
-template <int D>
-bool dispatch_kv(int kv, int G, const DecodeArgs& a, int part, dim3 grid, hipStream_t s) {
-    switch (kv) {
-        case PA_DTYPE_FP32: return dispatch_g<D, PA_DTYPE_FP32>(G, a, part, grid, s);
-        case PA_DTYPE_BF16: return dispatch_g<D, PA_DTYPE_BF16>(G, a, part, grid, s);
-        case PA_DTYPE_INT8: return dispatch_g<D, PA_DTYPE_INT8>(G, a, part, grid, s);
-        default: return false;
+    if (req == 0) {
+        int p = (max_len + 15) / 16;
+        p = (p + 255) / 256 * 256;
+        return p < 256 ? 256 : (p > kMaxPart ? kMaxPart : p);
     }
+    if (req < 64 || req > kMaxPart || req % 64 != 0) {
+        *err = "partition_size must be a multiple of 64 in [64, 4096]";
+        return -1;
+    }
+    return req;
 }
 
-int resolve_part(const pa_config* cfg) { return cfg->partition_size > 0 ? cfg->partition_size : kDefaultPart; }
-
-size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_context_len) {
-    const int part = resolve_part(cfg);
-    const int64_t max_parts = (static_cast<int64_t>(max_context_len) + part - 1) / part;
+size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
+    const int64_t max_parts = (static_cast<int64_t>(max_len) + part - 1) / part;
     if (max_parts <= 1 || num_seqs <= 0) return 0;
     const int64_t rows = static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts;
     return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float);
+}
+
+int32_t effective_max_len(int32_t max_context_len, int32_t max_blocks_per_seq) {
+    // Tokens beyond the table are never read, so the grid only needs to cover what the table holds.
+    const int64_t table_tokens = static_cast<int64_t>(max_blocks_per_seq) * pa::kBlockSize;
+    return max_context_len > table_tokens ? static_cast<int32_t>(table_tokens) : max_context_len;
+}
+
+// Resident workgroups per CU of a kernel, and CUs of the current device (queried once each;
+// read-only afterwards).
+template <typename K>
+int resident_wgs(K kernel) {
+    static int cached = [&] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+        return n;
+    }();
+    return cached;
+}
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int D, int KV, bool QF32>
+void launch_mfma(const DecodeArgs& a, dim3 grid, int num_seqs, hipStream_t s) {
+    if (num_seqs < kMaxPersistentSeqs) {
+        auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32>;
+        const int64_t upper = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+        int64_t nwg = static_cast<int64_t>(device_cus()) * resident_wgs(kern);
+        if (nwg > upper) nwg = upper;
+        if (nwg < 1) nwg = 1;
+        kern<<<static_cast<unsigned>(nwg), 256, 0, s>>>(a, num_seqs);
+    } else {
+        paged_decode_mfma_kernel<D, KV, QF32><<<grid, 256, 0, s>>>(a);
+    }
+}
+
+template <int D, int G>
+void launch_fp32(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+    if (a.part == 512) paged_decode_fp32_kernel<D, G, 512><<<grid, 256, 0, s>>>(a);
+    else paged_decode_fp32_kernel<D, G, 256><<<grid, 256, 0, s>>>(a);
+}
+
+template <int D>
+bool launch_decode(const pa_config* cfg, const DecodeArgs& a, dim3 grid, hipStream_t s) {
+    if (cfg->kv_dtype == PA_DTYPE_FP32) {
+        switch (a.group) {
+            case 1: launch_fp32<D, 1>(a, grid, s); return true;
+            case 2: launch_fp32<D, 2>(a, grid, s); return true;
+            case 4: launch_fp32<D, 4>(a, grid, s); return true;
+            case 8: launch_fp32<D, 8>(a, grid, s); return true;
+            default: return false;
+        }
+    }
+    const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
+    const int num_seqs = static_cast<int>(grid.z);
+    if (cfg->kv_dtype == PA_DTYPE_BF16) {
+        if (qf32) launch_mfma<D, PA_DTYPE_BF16, true>(a, grid, num_seqs, s);
+        else launch_mfma<D, PA_DTYPE_BF16, false>(a, grid, num_seqs, s);
+    } else {
+        if (qf32) launch_mfma<D, PA_DTYPE_INT8, true>(a, grid, num_seqs, s);
+        else launch_mfma<D, PA_DTYPE_INT8, false>(a, grid, num_seqs, s);
+    }
+    return true;
 }
 
 }  // namespace
@@ -353,10 +808,10 @@ pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs, int32
     if (!bytes) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_decode_workspace_size: bytes is null");
     if (num_seqs < 0 || max_context_len < 0)
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_decode_workspace_size: negative size");
-    const int part = resolve_part(cfg);
-    if (part != 256 && part != 512)
-        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_decode_workspace_size: partition_size must be 256 or 512");
-    *bytes = workspace_bytes_for(cfg, num_seqs, max_context_len);
+    std::string err;
+    const int part = resolve_part(cfg, max_context_len, &err);
+    if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_decode_workspace_size: " + err);
+    *bytes = workspace_bytes_for(cfg, num_seqs, max_context_len, part);
     return pa::clear_error();
 }
 
@@ -375,20 +830,20 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_paged_decode: null pointer");
     if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_paged_decode: int8 cache needs k_scale and v_scale");
-    const int part = resolve_part(cfg);
-    if (part != 256 && part != 512)
-        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: partition_size must be 256 or 512");
     const int G = cfg->num_q_heads / cfg->num_kv_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: Hq / Hkv must be 1, 2, 4 or 8");
+    const bool g_ok = cfg->kv_dtype == PA_DTYPE_FP32 ? (G == 1 || G == 2 || G == 4 || G == 8)
+                                                     : (G == 1 || G == 2 || G == 4 || G == 8 || G == 16);
+    if (!g_ok) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: unsupported Hq / Hkv ratio");
     if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: too many KV heads");
 
-    // Tokens beyond the table are never read, so the grid only needs to cover what the table holds.
-    int32_t max_len = max_context_len;
-    const int64_t table_tokens = static_cast<int64_t>(max_blocks_per_seq) * pa::kBlockSize;
-    if (max_len > table_tokens) max_len = static_cast<int32_t>(table_tokens);
+    const int32_t max_len = effective_max_len(max_context_len, max_blocks_per_seq);
+    std::string err;
+    // The partition length is resolved from the caller's max_context_len, exactly as
+    // pa_decode_workspace_size does, so both agree on the workspace layout.
+    const int part = resolve_part(cfg, max_context_len, &err);
+    if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: " + err);
     const int32_t max_parts = max_len > 0 ? (max_len + part - 1) / part : 1;
-    const size_t need = workspace_bytes_for(cfg, num_seqs, max_len);
+    const size_t need = workspace_bytes_for(cfg, num_seqs, max_len, part);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return pa::set_error(PA_ERROR_WORKSPACE_TOO_SMALL,
                              "pa_paged_decode: workspace of " + std::to_string(need) + " bytes required");
@@ -403,10 +858,12 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
     a.block_tables = block_tables;
     a.context_lens = context_lens;
     a.num_kv_heads = cfg->num_kv_heads;
+    a.group = G;
     a.max_blocks_per_seq = max_blocks_per_seq;
     a.num_blocks = cfg->num_blocks;
     a.max_context_len = max_len;
     a.max_parts = max_parts;
+    a.part = part;
     a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
     a.scale = pa::resolve_scale(cfg);
     if (need > 0) {
@@ -420,19 +877,18 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
     dim3 grid(max_parts, cfg->num_kv_heads, num_seqs);
     bool ok = false;
     switch (cfg->head_dim) {
-        case 64: ok = dispatch_kv<64>(cfg->kv_dtype, G, a, part, grid, s); break;
-        case 128: ok = dispatch_kv<128>(cfg->kv_dtype, G, a, part, grid, s); break;
-        case 256: ok = dispatch_kv<256>(cfg->kv_dtype, G, a, part, grid, s); break;
+        case 64: ok = launch_decode<64>(cfg, a, grid, s); break;
+        case 128: ok = launch_decode<128>(cfg, a, grid, s); break;
+        case 256: ok = launch_decode<256>(cfg, a, grid, s); break;
     }
     if (!ok) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: configuration not compiled");
     PA_HIP_CHECK(hipGetLastError());
     if (max_parts > 1) {
-        dim3 mgrid(cfg->num_q_heads, num_seqs);
-        const int threads = cfg->head_dim;
+        dim3 mgrid(cfg->num_kv_heads, num_seqs);
         switch (cfg->head_dim) {
-            case 64: paged_decode_merge_kernel<64><<<mgrid, threads, 0, s>>>(a, part); break;
-            case 128: paged_decode_merge_kernel<128><<<mgrid, threads, 0, s>>>(a, part); break;
-            default: paged_decode_merge_kernel<256><<<mgrid, threads, 0, s>>>(a, part); break;
+            case 64: paged_decode_merge_kernel<64><<<mgrid, 256, 0, s>>>(a); break;
+            case 128: paged_decode_merge_kernel<128><<<mgrid, 256, 0, s>>>(a); break;
+            default: paged_decode_merge_kernel<256><<<mgrid, 256, 0, s>>>(a); break;
         }
         PA_HIP_CHECK(hipGetLastError());
     }

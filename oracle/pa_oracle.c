@@ -249,8 +249,15 @@ static int orc_slot_valid(const pa_config* cfg, int64_t slot) {
     return slot >= 0 && slot < (int64_t)cfg->num_blocks * cfg->block_size;
 }
 
+/* Element (row `off` of block `blk`, KV head h, dim d) in the cache layout of pa_config:
+ * K tiles are row-major [block_size][head_dim], V tiles are dim-major [head_dim][block_size]. */
+static size_t orc_cache_index(const pa_config* cfg, int is_v, int64_t blk, int32_t h, int64_t off, int32_t d) {
+    const size_t tile = ((size_t)blk * cfg->num_kv_heads + h) * (size_t)cfg->block_size * cfg->head_dim;
+    return is_v ? tile + (size_t)d * cfg->block_size + off : tile + (size_t)off * cfg->head_dim + d;
+}
+
 /* One cache (K or V) of one append call. */
-static void orc_append_one(const pa_config* cfg, const void* x_new, const int64_t* sm,
+static void orc_append_one(const pa_config* cfg, int is_v, const void* x_new, const int64_t* sm,
                            int32_t n_tok, void* cache, float* scale, float* absmax) {
     const int32_t B = cfg->block_size, H = cfg->num_kv_heads, D = cfg->head_dim;
     if (cfg->kv_dtype != PA_DTYPE_INT8) {
@@ -260,7 +267,7 @@ static void orc_append_one(const pa_config* cfg, const void* x_new, const int64_
             for (int32_t h = 0; h < H; h++)
                 for (int32_t d = 0; d < D; d++) {
                     float x = orc_load_act(x_new, cfg->q_dtype, ((size_t)i * H + h) * D + d);
-                    size_t o = (((size_t)blk * H + h) * B + off) * D + d;
+                    size_t o = orc_cache_index(cfg, is_v, blk, h, off, d);
                     if (cfg->kv_dtype == PA_DTYPE_BF16) ((uint16_t*)cache)[o] = orc_bf16_from_f32(x);
                     else ((float*)cache)[o] = x;
                 }
@@ -304,7 +311,7 @@ static void orc_append_one(const pa_config* cfg, const void* x_new, const int64_
                 for (int32_t off = 0; off < B; off++) {
                     if (written & ((uint64_t)1 << off)) continue;
                     for (int32_t d = 0; d < D; d++) {
-                        size_t o = (((size_t)blk * H + h) * B + off) * D + d;
+                        size_t o = orc_cache_index(cfg, is_v, blk, h, off, d);
                         c8[o] = orc_quantize_symmetric(orc_dequantize(c8[o], old_scale), cur_scale);
                     }
                 }
@@ -315,7 +322,7 @@ static void orc_append_one(const pa_config* cfg, const void* x_new, const int64_
                 int64_t off = sm[t] % B;
                 for (int32_t d = 0; d < D; d++) {
                     float x = orc_load_act(x_new, cfg->q_dtype, ((size_t)t * H + h) * D + d);
-                    c8[(((size_t)blk * H + h) * B + off) * D + d] = orc_quantize_symmetric(x, cur_scale);
+                    c8[orc_cache_index(cfg, is_v, blk, h, off, d)] = orc_quantize_symmetric(x, cur_scale);
                 }
             }
         }
@@ -331,8 +338,8 @@ int orc_kv_append(const pa_config* cfg, const void* k_new, const void* v_new,
     if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache) return -1;
     if (cfg->block_size <= 0 || cfg->block_size > 64) return -1;
     if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale || !k_absmax || !v_absmax)) return -1;
-    orc_append_one(cfg, k_new, slot_mapping, n_tok, k_cache, k_scale, k_absmax);
-    orc_append_one(cfg, v_new, slot_mapping, n_tok, v_cache, v_scale, v_absmax);
+    orc_append_one(cfg, 0, k_new, slot_mapping, n_tok, k_cache, k_scale, k_absmax);
+    orc_append_one(cfg, 1, v_new, slot_mapping, n_tok, v_cache, v_scale, v_absmax);
     return 0;
 }
 
@@ -342,7 +349,7 @@ int orc_kv_append(const pa_config* cfg, const void* k_new, const void* v_new,
  * DecodeOrchestrator.GatherDecodeKeys (Layers/PagedAttentionLayer.cs:368-389,
  * Phases/DecodeOrchestrator.cs:111-123): token t lives at block table[t / B], row t % B.
  * KV head h / G feeds query head h (GQA by head repetition). Tokens in an invalid block read 0. */
-static void orc_gather(const pa_config* cfg, const void* cache, const float* scales,
+static void orc_gather(const pa_config* cfg, int is_v, const void* cache, const float* scales,
                        const int32_t* table, int32_t max_blocks, int32_t T, float* dst) {
     const int32_t B = cfg->block_size, Hkv = cfg->num_kv_heads, Hq = cfg->num_q_heads, D = cfg->head_dim;
     const int32_t G = Hq / Hkv;
@@ -354,13 +361,13 @@ static void orc_gather(const pa_config* cfg, const void* cache, const float* sca
             int32_t kh = h / G;
             float* row = dst + ((size_t)t * Hq + h) * D;
             if (!valid) { memset(row, 0, sizeof(float) * (size_t)D); continue; }
-            size_t base = (((size_t)blk * Hkv + kh) * B + (t % B)) * (size_t)D;
             for (int32_t d = 0; d < D; d++) {
+                size_t o = orc_cache_index(cfg, is_v, blk, kh, t % B, d);
                 float x;
-                if (cfg->kv_dtype == PA_DTYPE_BF16) x = orc_f32_from_bf16(((const uint16_t*)cache)[base + d]);
+                if (cfg->kv_dtype == PA_DTYPE_BF16) x = orc_f32_from_bf16(((const uint16_t*)cache)[o]);
                 else if (cfg->kv_dtype == PA_DTYPE_INT8)
-                    x = orc_dequantize(((const int8_t*)cache)[base + d], scales[(size_t)blk * Hkv + kh]);
-                else x = ((const float*)cache)[base + d];
+                    x = orc_dequantize(((const int8_t*)cache)[o], scales[(size_t)blk * Hkv + kh]);
+                else x = ((const float*)cache)[o];
                 row[d] = x;
             }
         }
@@ -402,8 +409,8 @@ int orc_paged_decode(const pa_config* cfg, float* out, const void* q,
         if (!qs || !ks || !vs) { free(qs); free(ks); free(vs); err |= 1; continue; }
         for (int32_t i = 0; i < Hq * D; i++) qs[i] = orc_load_act(q, cfg->q_dtype, (size_t)s * Hq * D + i);
         const int32_t* table = block_tables + (size_t)s * max_blocks_per_seq;
-        orc_gather(cfg, k_cache, k_scale, table, max_blocks_per_seq, T, ks);
-        orc_gather(cfg, v_cache, v_scale, table, max_blocks_per_seq, T, vs);
+        orc_gather(cfg, 0, k_cache, k_scale, table, max_blocks_per_seq, T, ks);
+        orc_gather(cfg, 1, v_cache, v_scale, table, max_blocks_per_seq, T, vs);
         err |= orc_sdpa(qs, ks, vs, o, 1, 1, T, Hq, D, PA_PHASE_DECODE, cfg->scale, 0) != 0;
         free(qs); free(ks); free(vs);
     }
@@ -444,8 +451,8 @@ int orc_chunked_prefill(const pa_config* cfg, float* out, const void* q,
         for (size_t i = 0; i < (size_t)L * Hq * D; i++)
             qs[i] = orc_load_act(q, cfg->q_dtype, (size_t)q_start_loc[s] * Hq * D + i);
         const int32_t* table = block_tables + (size_t)s * max_blocks_per_seq;
-        orc_gather(cfg, k_cache, k_scale, table, max_blocks_per_seq, T, ks);
-        orc_gather(cfg, v_cache, v_scale, table, max_blocks_per_seq, T, vs);
+        orc_gather(cfg, 0, k_cache, k_scale, table, max_blocks_per_seq, T, ks);
+        orc_gather(cfg, 1, v_cache, v_scale, table, max_blocks_per_seq, T, vs);
         int phase = no_mask ? PA_PHASE_PREFILL : PA_PHASE_DECODE;
         int force = (!no_mask && !literal) ? 1 : 0;
         err |= orc_sdpa(qs, ks, vs, o, 1, L, T, Hq, D, phase, cfg->scale, force) != 0;
