@@ -3,14 +3,15 @@
 
 Step = one decode layer-step of the C2 configuration (Llama-3-8B layer shape: Hq=32, Hkv=8,
 D=128, bf16 KV, block 16, batch 64, contexts log-uniform in [128, 4096], shuffled physical
-blocks): append the new token's K/V of every sequence into the paged cache (pa_kv_append), then
-attend over each sequence's whole context (pa_paged_decode). Inputs are resident in HBM before
-timing starts; all launches go through the C-ABI of libpa_hip.so on one pa_stream and are timed
-with pa_events on that stream.
+blocks): append the new token's K/V of every sequence into the paged cache and attend over each
+sequence's whole context, as one pa_paged_decode_append call (the fused kernel plus the split-K
+merge). Inputs are resident in HBM before timing starts; all launches go through the C-ABI of
+libpa_hip.so on one pa_stream and are timed with pa_events on that stream.
 
 Output: one JSON line. `value` is the achieved algorithmic HBM bandwidth of the whole step
 (distinct KV bytes read + Q + O + block tables + the appended K/V, divided by the step time);
-tokens/s per layer and us per layer-step ride along. `roofline` covers pa_paged_decode alone.
+tokens/s per layer and us per layer-step ride along. `roofline` covers the same call; the
+two-call path (pa_kv_append + pa_paged_decode) is timed beside it for reference.
 `cpu_baseline` times the CPU oracle (a C restatement of the reference's StandardPagedAttentionKernel
 with its per-sequence decode loop) on a bounded sample of the same batch, on this host.
 """
@@ -172,46 +173,48 @@ def main():
     S, mcl = w.num_seqs, w.max_context_len
     out = torch.empty((S, w.num_q_heads, w.head_dim), dtype=torch.float32, device="cuda:0")
     wsb = pa.decode_workspace_size(cfg, S, mcl)
-    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device="cuda:0")
+    ws = torch.zeros((max(wsb, 1),), dtype=torch.uint8, device="cuda:0")  # zero-filled once
     torch.cuda.synchronize()
 
-    def append():
-        pa.kv_append(stream, cfg, inp["k_new"], inp["v_new"], inp["slots"], S, inp["k_cache"], inp["v_cache"])
+    def step():
+        pa.paged_decode_append(stream, cfg, out, inp["q"], inp["k_new"], inp["v_new"], inp["k_cache"],
+                               inp["v_cache"], None, None, None, None, inp["tables"], inp["lens"], S,
+                               w.max_blocks, mcl, ws, wsb)
 
-    def decode():
+    def two_call_step():
+        pa.kv_append(stream, cfg, inp["k_new"], inp["v_new"], inp["slots"], S, inp["k_cache"], inp["v_cache"])
         pa.paged_decode(stream, cfg, out, inp["q"], inp["k_cache"], inp["v_cache"], None, None,
                         inp["tables"], inp["lens"], S, w.max_blocks, mcl, ws, wsb)
 
-    for _ in range(args.warmup):
-        append()
-        decode()
-    stream.synchronize()
+    def timed(fn, n):
+        e0, e1 = pa.Event(dev), pa.Event(dev)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / n
+        e0.destroy()
+        e1.destroy()
+        return ms
 
-    e0, e1, e2, e3 = (pa.Event(dev) for _ in range(4))
-    # Whole layer-steps (append + decode).
+    for _ in range(args.warmup):
+        step()
+    stream.synchronize()
+    step_ms = timed(step, args.steps)
+    for _ in range(args.warmup):
+        two_call_step()
+    two_call_ms = timed(two_call_step, args.steps)
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        append()
-        decode()
-    e1.record(stream)
-    e1.synchronize()
-    step_ms = e0.elapsed_ms(e1) / args.steps
-    # pa_paged_decode alone (the dominant kernel's launches) for the roofline.
-    e2.record(stream)
-    for _ in range(args.steps):
-        decode()
-    e3.record(stream)
-    e3.synchronize()
-    decode_ms = e2.elapsed_ms(e3) / args.steps
-    torch.cuda.synchronize()
-    log(f"[bench] step {step_ms * 1e3:.2f} us, decode {decode_ms * 1e3:.2f} us")
+    log(f"[bench] fused step {step_ms * 1e3:.2f} us, two-call step {two_call_ms * 1e3:.2f} us")
 
     dec_bytes = w.decode_algorithmic_bytes()
-    app_bytes = 2 * S * w.num_kv_heads * w.head_dim * 2 * 2 + S * 8  # read + write new K/V, slots
+    # the appended token: new K/V read (bf16) + written into the cache
+    app_bytes = 2 * S * w.num_kv_heads * w.head_dim * 2 * 2
     step_bytes = dec_bytes + app_bytes
     value = step_bytes / (step_ms * 1e-3) / 1e9
-    achieved = dec_bytes / (decode_ms * 1e-3) / 1e9
+    achieved = value
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -243,22 +246,21 @@ def main():
         "tokens_per_s_per_layer": round(S / (step_ms * 1e-3), 1),
         "us_per_layer_step": round(step_ms * 1e3, 3),
         "roofline": {
-            "kernel": "pa_paged_decode (paged_decode_kernel + partition merge)",
+            "kernel": "pa_paged_decode_append (fused append + paged decode kernel, then split-K merge)",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": None,
-            "algorithmic_bytes_per_launch": int(dec_bytes),
-            "us_per_launch": round(decode_ms * 1e3, 3),
+            "algorithmic_bytes_per_launch": int(step_bytes),
+            "us_per_launch": round(step_ms * 1e3, 3),
         },
+        "two_call_us_per_layer_step": round(two_call_ms * 1e3, 3),
         "cpu_baseline": cpu,
         "device": {"name": props.name.decode(), "arch": props.arch.decode(), "cus": props.compute_units},
     }
     stream.destroy()
-    for e in (e0, e1, e2, e3):
-        e.destroy()
     dev.close()
     print(json.dumps(res), flush=True)
 

@@ -186,7 +186,8 @@ pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg,
                        float* k_scale, float* v_scale, float* k_absmax, float* v_absmax);
 
 /* Bytes of device workspace pa_paged_decode needs for this shape (0 when no sequence needs more
- * than one partition). */
+ * than one partition). The workspace holds per-partition partial results of one call; its
+ * contents need no initialisation, and calls that share a workspace must not run concurrently. */
 pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs,
                                    int32_t max_context_len, size_t* bytes);
 
@@ -208,6 +209,23 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
                           const int32_t* block_tables, const int32_t* context_lens,
                           int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
                           void* workspace, size_t workspace_bytes);
+
+/* Fused decode layer-step: appends the token at position context_lens[s] - 1 of every sequence
+ * (k_new/v_new [num_seqs][num_kv_heads][head_dim] of cfg->q_dtype) into the cache, then runs
+ * pa_paged_decode. Cache bytes, int8 scales and absmax after the call are exactly those of
+ * pa_kv_append with slot_mapping[s] = block_tables[s][(T-1)/16] * 16 + (T-1) % 16 followed by
+ * pa_paged_decode; for bf16/int8 caches both happen in one kernel (the workgroup that owns a
+ * sequence's last block patches the new token into its registers and the cache). No reference
+ * counterpart: the reference appends (PagedAttentionLayer.UpdateKVCache, Layers/
+ * PagedAttentionLayer.cs:244-296) and decodes (DecodeOrchestrator.ComputeDecodeAttention,
+ * Phases/DecodeOrchestrator.cs:64-80) in two steps; this is those two steps in one launch.
+ * Sequences with context_len <= 0 append nothing and produce zeros. */
+pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                 const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                                 float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
+                                 void* workspace, size_t workspace_bytes);
 
 /* Chunked prefill: prefill sequence s has chunk_len[s] = q_start_loc[s+1] - q_start_loc[s] new
  * query tokens at absolute positions prefix_lens[s] + i; the chunk's K/V must already be appended,

@@ -43,6 +43,11 @@ struct DecodeArgs {
     float* ws_o;  // [num_seqs][Hq][max_parts][D]
     float* ws_m;  // [num_seqs][Hq][max_parts]
     float* ws_l;  // [num_seqs][Hq][max_parts]
+    // fused append (pa_paged_decode_append): the token at position context_len - 1
+    const void* k_new;  // [num_seqs][Hkv][D] of the activation dtype
+    const void* v_new;
+    float* k_absmax;    // int8 caches: running absmax / scale per (block, KV head), updated
+    float* v_absmax;
     int32_t num_kv_heads;
     int32_t group;  // G = Hq / Hkv
     int32_t max_blocks_per_seq;
@@ -106,6 +111,70 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Log-sum-exp merge of the partitions of one (sequence, KV head): wave w takes query heads
+// w, w + 4, ... Partition statistics are read 64 at a time (one per lane); the weighted sum over
+// partitions issues its loads in groups of 8 so their latencies overlap.
+template <int D>
+__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts) {
+    constexpr int DPL = D / 64;  // dims per lane
+    constexpr int CHUNK = 16;    // partitions whose loads are issued together
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = a.group;
+    for (int g = wave; g < G; g += 4) {
+        const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
+        const int64_t base = row * a.max_parts;
+        float M = -INFINITY, L = 0.0f;
+        float o[DPL];
+#pragma unroll
+        for (int k = 0; k < DPL; k++) o[k] = 0.0f;
+        // Running log-sum-exp over chunks of partitions; within a chunk every load (m, l and the
+        // partial outputs) is issued before any is used.
+        for (int p0 = 0; p0 < nparts; p0 += CHUNK) {
+            const int cnt = min(CHUNK, nparts - p0);
+            float pm[CHUNK], pl[CHUNK], po[CHUNK][DPL];
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) {
+                const bool ok = u < cnt;
+                const int64_t pi = base + p0 + (ok ? u : 0);
+                pm[u] = ok ? a.ws_m[pi] : -INFINITY;
+                pl[u] = ok ? a.ws_l[pi] : 0.0f;
+#pragma unroll
+                for (int k = 0; k < DPL; k++) po[u][k] = ok ? a.ws_o[pi * D + lane + 64 * k] : 0.0f;
+            }
+            float cm = M;
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) cm = fmaxf(cm, pm[u]);
+            const float r = __expf(M - cm);  // rescale of what was accumulated (0 on the first chunk)
+            L *= r;
+#pragma unroll
+            for (int k = 0; k < DPL; k++) o[k] *= r;
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) {
+                const float w = __expf(pm[u] - cm);
+                L += pl[u] * w;
+#pragma unroll
+                for (int k = 0; k < DPL; k++) o[k] += po[u][k] * w;
+            }
+            M = cm;
+        }
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
+    }
+}
+
+// Separate merge pass (fp32 caches): one workgroup per (KV head, sequence).
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
+    const int kvh = blockIdx.x, seq = blockIdx.y;
+    const int T = clamp_len(a, seq);
+    if (T <= 0) return;
+    const int nparts = (T + a.part - 1) / a.part;
+    if (nparts <= 1) return;
+    merge_partitions<D>(a, seq, kvh, nparts);
+}
+
 __device__ __forceinline__ bf16x8_t k_operand(const uint4& r) { return __builtin_bit_cast(bf16x8_t, r); }
 __device__ __forceinline__ bf16x8_t k_operand(const uint2& r) {
     const uint4 p = make_uint4(pack_i8pair(r.x, 0), pack_i8pair(r.x, 2), pack_i8pair(r.y, 0), pack_i8pair(r.y, 2));
@@ -115,6 +184,151 @@ __device__ __forceinline__ s16x4_t v_operand(const uint2& r) { return __builtin_
 __device__ __forceinline__ s16x4_t v_operand(const uint32_t& r) {
     const uint2 p = make_uint2(pack_i8pair(r, 0), pack_i8pair(r, 2));
     return __builtin_bit_cast(s16x4_t, p);
+}
+
+// ---- fused append: the new token (row r of the sequence's last block) enters the owning wave's
+// registers and the cache. Values and cache bytes are those of pa_kv_append for that one token.
+__device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
+    return f32 ? static_cast<const float*>(p)[i] : pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int D, bool QF32>
+__device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t tile, int64_t src, int r, int q4,
+                                                 int n, uint4 (&kr)[D / 32], uint2 (&vr)[D / 16]) {
+    constexpr int NSLAB = D / 32, NT = D / 16;
+    uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache));
+    uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache));
+    if (n == r) {  // K row r: dims 32s + 8q4 .. +8 of this lane
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++) {
+            const int d0 = 32 * sl + 8 * q4;
+            uint4 v;
+            if constexpr (QF32) {
+                const float* x = static_cast<const float*>(a.k_new) + src + d0;
+                v = make_uint4(pack_bf16_trunc(x[0], x[1]), pack_bf16_trunc(x[2], x[3]),
+                               pack_bf16_trunc(x[4], x[5]), pack_bf16_trunc(x[6], x[7]));
+            } else {
+                v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.k_new) + src + d0);
+            }
+            kr[sl] = v;
+            *reinterpret_cast<uint4*>(kc + tile + r * D + d0) = v;
+        }
+    }
+    if (q4 == (r >> 2)) {  // V column r: element r & 3 of this lane's 4-token run, dims 16t + n
+        const int e = r & 3;
+        const uint32_t sh = (e & 1) * 16;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int d = 16 * t + n;
+            uint32_t b;
+            if constexpr (QF32) b = __float_as_uint(static_cast<const float*>(a.v_new)[src + d]) >> 16;
+            else b = static_cast<const uint16_t*>(a.v_new)[src + d];
+            const uint32_t mask = ~(0xffffu << sh);
+            if (e < 2) vr[t].x = (vr[t].x & mask) | (b << sh);
+            else vr[t].y = (vr[t].y & mask) | (b << sh);
+            vc[tile + d * 16 + r] = static_cast<uint16_t>(b);
+        }
+    }
+}
+
+__device__ __forceinline__ int code_at(uint32_t w, int k) { return static_cast<int32_t>(w << (24 - 8 * k)) >> 24; }
+__device__ __forceinline__ uint32_t with_code(uint32_t w, int k, int8_t c) {
+    return (w & ~(0xffu << (8 * k))) | (static_cast<uint32_t>(static_cast<uint8_t>(c)) << (8 * k));
+}
+
+// int8: the owning wave holds the whole (block, head) tile in registers (K: 8 codes per lane per
+// 32-dim slab, V: 4 codes per lane per 16-dim tile), so the scale growth and requantisation of
+// pa_kv_append run in place. Returns the tile's K and V scales after the append.
+template <int D, bool QF32>
+__device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t tile, int64_t src, int64_t sidx,
+                                                 int r, int q4, int n, uint2 (&kr)[D / 32], uint32_t (&vr)[D / 16],
+                                                 float& k_scale_out, float& v_scale_out) {
+#pragma clang fp contract(off)
+    constexpr int NSLAB = D / 32, NT = D / 16;
+    int8_t* kc = static_cast<int8_t*>(const_cast<void*>(a.k_cache));
+    int8_t* vc = static_cast<int8_t*>(const_cast<void*>(a.v_cache));
+    float* kscale = const_cast<float*>(a.k_scale);
+    float* vscale = const_cast<float*>(a.v_scale);
+    const bool fresh = r == 0;  // writing row 0 starts the block afresh
+    const int lane = threadIdx.x & 63;
+    // ---------------- K ----------------
+    {
+        float x[NSLAB][8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x[sl][e] = n == r ? act_at(a.k_new, QF32, src + 32 * sl + 8 * q4 + e) : 0.0f;
+                const float ax = fabsf(x[sl][e]);
+                amax = ax > amax ? ax : amax;
+            }
+        amax = pa::wave_max(amax);
+        const float old_amax = fresh ? 0.0f : a.k_absmax[sidx];
+        const float old_scale = fresh ? 0.0f : kscale[sidx];
+        const bool grow = !fresh && amax > old_amax;
+        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++) {
+            uint32_t w[2] = {kr[sl].x, kr[sl].y};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                int8_t c;
+                if (n == r) c = pa::quantize_symmetric(x[sl][e], sc);
+                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w[e >> 2], e & 3)) * old_scale, sc);
+                else c = static_cast<int8_t>(code_at(w[e >> 2], e & 3));
+                w[e >> 2] = with_code(w[e >> 2], e & 3, c);
+            }
+            kr[sl] = make_uint2(w[0], w[1]);
+            if (grow || n == r) *reinterpret_cast<uint2*>(kc + tile + n * D + 32 * sl + 8 * q4) = kr[sl];
+        }
+        if (lane == 0 && (fresh || grow)) {
+            a.k_absmax[sidx] = amax;
+            kscale[sidx] = sc;
+        }
+        k_scale_out = sc;
+    }
+    // ---------------- V (tile is [D][16]: lane holds tokens 4q4..4q4+3 of dim 16t+n) ----------------
+    {
+        const bool mine = q4 == (r >> 2);
+        const int er = r & 3;
+        float x[NT];
+        float amax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            x[t] = mine ? act_at(a.v_new, QF32, src + 16 * t + n) : 0.0f;
+            const float ax = fabsf(x[t]);
+            amax = ax > amax ? ax : amax;
+        }
+        amax = pa::wave_max(amax);
+        const float old_amax = fresh ? 0.0f : a.v_absmax[sidx];
+        const float old_scale = fresh ? 0.0f : vscale[sidx];
+        const bool grow = !fresh && amax > old_amax;
+        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            uint32_t w = vr[t];
+            int8_t newc = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool is_new = mine && e == er;
+                int8_t c;
+                if (is_new) c = newc = pa::quantize_symmetric(x[t], sc);
+                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w, e)) * old_scale, sc);
+                else c = static_cast<int8_t>(code_at(w, e));
+                w = with_code(w, e, c);
+            }
+            vr[t] = w;
+            int8_t* dst = vc + tile + (16 * t + n) * 16;
+            if (grow) *reinterpret_cast<uint32_t*>(dst + 4 * q4) = w;
+            else if (mine) dst[r] = newc;
+        }
+        if (lane == 0 && (fresh || grow)) {
+            a.v_absmax[sidx] = amax;
+            vscale[sidx] = sc;
+        }
+        v_scale_out = sc;
+    }
 }
 
 // Online-softmax rescaling is deferred until a block's max exceeds the running max by more than
@@ -130,7 +344,7 @@ struct MfmaShared {
 };
 
 // One work item: (sequence, KV head, partition). Called by all 256 threads of a workgroup.
-template <int D, int KV, bool QF32>
+template <int D, int KV, bool QF32, bool APPEND>
 __device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh, int part, MfmaShared& sh,
                                           float (*s_x)[D][16]) {
     using Raw = MfmaRaw<KV>;
@@ -159,6 +373,12 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh,
 
     // This wave's blocks: lb0 + wave + 4j, j < nb. Lane j holds block j's id (and int8 scales).
     const int lb0 = tok0 / 16;
+    // Fused append: the last block of the sequence belongs to wave (rel & 3), iteration rel >> 2.
+    int j_app = -1;
+    if constexpr (APPEND) {
+        const int rel = (T - 1) / 16 - lb0;
+        if (part == nparts - 1 && (rel & 3) == wave) j_app = rel >> 2;
+    }
     const int nblk = (tok_end - tok0 + 15) / 16;
     const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;
     const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
@@ -234,7 +454,25 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh,
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], int j) {
+    auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
+        float ks = 1.0f, vfac = 1.0f;
+        if constexpr (KV == PA_DTYPE_INT8) {
+            ks = readlane_f(my_ks, j);
+            vfac = readlane_f(my_vs, j);
+        }
+        if constexpr (APPEND) {
+            const int bid = __builtin_amdgcn_readlane(my_bid, j);
+            if (j == j_app && bid >= 0) {
+                const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * TILE;
+                const int64_t src = (static_cast<int64_t>(seq) * Hkv + kvh) * D;
+                const int r = (T - 1) & 15;
+                if constexpr (KV == PA_DTYPE_INT8)
+                    append_int8_regs<D, QF32>(a, tile, src, static_cast<int64_t>(bid) * Hkv + kvh, r, q4, n, kr, vr,
+                                              ks, vfac);
+                else
+                    append_bf16_regs<D, QF32>(a, tile, src, r, q4, n, kr, vr);
+            }
+        }
         // S^T[token 4q4+i][head n]
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -242,11 +480,6 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh,
             const bf16x8_t kop = k_operand(kr[sl]);
             s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
             if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
-        }
-        float ks = 1.0f, vfac = 1.0f;
-        if constexpr (KV == PA_DTYPE_INT8) {
-            ks = readlane_f(my_ks, j);
-            vfac = readlane_f(my_vs, j);
         }
         const int tbase = (lb0 + wave + 4 * j) * 16 + 4 * q4;
         float sc[4];
@@ -395,17 +628,17 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, int seq, int kvh,
 }
 
 // Grid mode: one workgroup per (partition, KV head, sequence).
-template <int D, int KV, bool QF32>
+template <int D, int KV, bool QF32, bool APPEND>
 __global__ __launch_bounds__(256, 2) void paged_decode_mfma_kernel(const DecodeArgs a) {
     __shared__ MfmaShared sh;
     __shared__ float s_x[2][D][16];
-    mfma_item<D, KV, QF32>(a, blockIdx.z, blockIdx.y, blockIdx.x, sh, s_x);
+    mfma_item<D, KV, QF32, APPEND>(a, blockIdx.z, blockIdx.y, blockIdx.x, sh, s_x);
 }
 
 // Persistent mode: gridDim.x workgroups walk the compacted list of non-empty items
 // (sequence s owns items pref[s]*Hkv .. pref[s+1]*Hkv - 1, KV head fastest), item w, w + grid, ...
 // Every workgroup leaves its loop after a bounded number of items.
-template <int D, int KV, bool QF32>
+template <int D, int KV, bool QF32, bool APPEND>
 __global__ __launch_bounds__(256, 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a, int32_t num_seqs) {
     __shared__ MfmaShared sh;
     __shared__ float s_x[2][D][16];
@@ -457,7 +690,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_mfma_persistent_kernel(co
         const int kvh = static_cast<int>(item - static_cast<int64_t>(pi) * Hkv);
         // Items only increase, so the owning sequence is found by scanning forward.
         while (seq + 1 < num_seqs && sh.pref[seq + 1] <= pi) seq++;
-        mfma_item<D, KV, QF32>(a, seq, kvh, pi - sh.pref[seq], sh, s_x);
+        mfma_item<D, KV, QF32, APPEND>(a, seq, kvh, pi - sh.pref[seq], sh, s_x);
     }
 }
 
@@ -630,67 +863,6 @@ __global__ __launch_bounds__(256) void paged_decode_fp32_kernel(const DecodeArgs
 }
 
 // ================================================================================================
-// Log-sum-exp merge of the partitions of one (sequence, KV head): one wave per query head.
-// Partition statistics are read 64 at a time (one per lane); the weighted sum over partitions
-// issues its loads in groups of 8 so their latencies overlap.
-// ================================================================================================
-template <int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
-    constexpr int DPL = D / 64;  // dims per lane
-    const int kvh = blockIdx.x, seq = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int G = a.group;
-    const int T = clamp_len(a, seq);
-    if (T <= 0) return;
-    const int nparts = (T + a.part - 1) / a.part;
-    if (nparts <= 1) return;
-    for (int g = wave; g < G; g += 4) {
-        const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
-        const int64_t base = row * a.max_parts;
-        float M = -INFINITY;
-        for (int p0 = 0; p0 < nparts; p0 += 64)
-            if (p0 + lane < nparts) M = fmaxf(M, a.ws_m[base + p0 + lane]);
-        M = pa::wave_max(M);
-        float L = 0.0f;
-        float o[DPL];
-#pragma unroll
-        for (int k = 0; k < DPL; k++) o[k] = 0.0f;
-        for (int p0 = 0; p0 < nparts; p0 += 64) {
-            const int cnt = min(64, nparts - p0);
-            float w = 0.0f;
-            if (lane < cnt) {
-                w = __expf(a.ws_m[base + p0 + lane] - M);
-                L += a.ws_l[base + p0 + lane] * w;
-            }
-            const float* src = a.ws_o + (base + p0) * D + lane;
-            int p = 0;
-            for (; p + 8 <= cnt; p += 8) {
-                float v[8][DPL];
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-#pragma unroll
-                    for (int k = 0; k < DPL; k++) v[u][k] = src[(p + u) * D + 64 * k];
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float wu = readlane_f(w, p + u);
-#pragma unroll
-                    for (int k = 0; k < DPL; k++) o[k] += v[u][k] * wu;
-                }
-            }
-            for (; p < cnt; p++) {
-                const float wu = readlane_f(w, p);
-#pragma unroll
-                for (int k = 0; k < DPL; k++) o[k] += src[p * D + 64 * k] * wu;
-            }
-        }
-        L = pa::wave_sum(L);
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
-    }
-}
-
 // ---- host side ---------------------------------------------------------------------------------
 constexpr int kMaxPart = 4096;  // a wave's block ids must fit one VGPR (64 lanes x 4 waves x 16)
 
@@ -717,6 +889,7 @@ int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
     return req;
 }
 
+// Workspace: [o fp32 rows*D][m fp32 rows][l fp32 rows] with rows = num_seqs * Hq * max_parts.
 size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
     const int64_t max_parts = (static_cast<int64_t>(max_len) + part - 1) / part;
     if (max_parts <= 1 || num_seqs <= 0) return 0;
@@ -754,17 +927,39 @@ int device_cus() {
     return cus[dev];
 }
 
-template <int D, int KV, bool QF32>
+template <int D, int KV, bool QF32, bool APPEND>
 void launch_mfma(const DecodeArgs& a, dim3 grid, int num_seqs, hipStream_t s) {
     if (num_seqs < kMaxPersistentSeqs) {
-        auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32>;
+        auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND>;
         const int64_t upper = static_cast<int64_t>(grid.x) * grid.y * grid.z;
         int64_t nwg = static_cast<int64_t>(device_cus()) * resident_wgs(kern);
         if (nwg > upper) nwg = upper;
         if (nwg < 1) nwg = 1;
         kern<<<static_cast<unsigned>(nwg), 256, 0, s>>>(a, num_seqs);
     } else {
-        paged_decode_mfma_kernel<D, KV, QF32><<<grid, 256, 0, s>>>(a);
+        paged_decode_mfma_kernel<D, KV, QF32, APPEND><<<grid, 256, 0, s>>>(a);
+    }
+}
+
+// fp32 caches, fused entry point: append the token at position context_len - 1 of every
+// sequence (one workgroup per sequence, K row and V column of every KV head), before the decode.
+__global__ __launch_bounds__(256) void append_last_token_fp32_kernel(const DecodeArgs a, int32_t head_dim) {
+    const int seq = blockIdx.x;
+    const int T = clamp_len(a, seq);
+    if (T <= 0) return;
+    const int bid = a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + (T - 1) / 16];
+    if (bid < 0 || bid >= a.num_blocks) return;
+    const int r = (T - 1) & 15;
+    const int Hkv = a.num_kv_heads, n = Hkv * head_dim;
+    float* kc = static_cast<float*>(const_cast<void*>(a.k_cache));
+    float* vc = static_cast<float*>(const_cast<void*>(a.v_cache));
+    const bool f32 = !a.q_bf16;
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+        const int h = idx / head_dim, d = idx - h * head_dim;
+        const int64_t src = static_cast<int64_t>(seq) * n + idx;
+        const int64_t tile = (static_cast<int64_t>(bid) * Hkv + h) * 16 * head_dim;
+        kc[tile + r * head_dim + d] = act_at(a.k_new, f32, src);
+        vc[tile + d * 16 + r] = act_at(a.v_new, f32, src);
     }
 }
 
@@ -774,9 +969,10 @@ void launch_fp32(const DecodeArgs& a, dim3 grid, hipStream_t s) {
     else paged_decode_fp32_kernel<D, G, 256><<<grid, 256, 0, s>>>(a);
 }
 
-template <int D>
+template <int D, bool APPEND>
 bool launch_decode(const pa_config* cfg, const DecodeArgs& a, dim3 grid, hipStream_t s) {
     if (cfg->kv_dtype == PA_DTYPE_FP32) {
+        if (APPEND) append_last_token_fp32_kernel<<<grid.z, 256, 0, s>>>(a, D);
         switch (a.group) {
             case 1: launch_fp32<D, 1>(a, grid, s); return true;
             case 2: launch_fp32<D, 2>(a, grid, s); return true;
@@ -788,11 +984,11 @@ bool launch_decode(const pa_config* cfg, const DecodeArgs& a, dim3 grid, hipStre
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     const int num_seqs = static_cast<int>(grid.z);
     if (cfg->kv_dtype == PA_DTYPE_BF16) {
-        if (qf32) launch_mfma<D, PA_DTYPE_BF16, true>(a, grid, num_seqs, s);
-        else launch_mfma<D, PA_DTYPE_BF16, false>(a, grid, num_seqs, s);
+        if (qf32) launch_mfma<D, PA_DTYPE_BF16, true, APPEND>(a, grid, num_seqs, s);
+        else launch_mfma<D, PA_DTYPE_BF16, false, APPEND>(a, grid, num_seqs, s);
     } else {
-        if (qf32) launch_mfma<D, PA_DTYPE_INT8, true>(a, grid, num_seqs, s);
-        else launch_mfma<D, PA_DTYPE_INT8, false>(a, grid, num_seqs, s);
+        if (qf32) launch_mfma<D, PA_DTYPE_INT8, true, APPEND>(a, grid, num_seqs, s);
+        else launch_mfma<D, PA_DTYPE_INT8, false, APPEND>(a, grid, num_seqs, s);
     }
     return true;
 }
@@ -815,38 +1011,47 @@ pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs, int32
     return pa::clear_error();
 }
 
-pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
-                          const void* k_cache, const void* v_cache, const float* k_scale,
-                          const float* v_scale, const int32_t* block_tables, const int32_t* context_lens,
-                          int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
-                          void* workspace, size_t workspace_bytes) {
-    pa_status st = pa::check_config(cfg, "pa_paged_decode");
+}  // extern "C"
+
+namespace {
+
+pa_status decode_impl(const char* fn, bool append, pa_stream* stream, const pa_config* cfg, float* out,
+                      const void* q, const void* k_new, const void* v_new, const void* k_cache,
+                      const void* v_cache, const float* k_scale, const float* v_scale, float* k_absmax,
+                      float* v_absmax, const int32_t* block_tables, const int32_t* context_lens,
+                      int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len, void* workspace,
+                      size_t workspace_bytes) {
+    const std::string f(fn);
+    pa_status st = pa::check_config(cfg, fn);
     if (st != PA_SUCCESS) return st;
     if (num_seqs < 0 || max_blocks_per_seq < 0 || max_context_len < 0)
-        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_paged_decode: negative size");
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": negative size");
     if (num_seqs == 0) return pa::clear_error();
-    if (num_seqs > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: num_seqs > 65535");
+    if (num_seqs > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": num_seqs > 65535");
     if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens)
-        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_paged_decode: null pointer");
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": null pointer");
+    if (append && (!k_new || !v_new)) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": null k_new/v_new");
     if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
-        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_paged_decode: int8 cache needs k_scale and v_scale");
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": int8 cache needs k_scale and v_scale");
+    if (append && cfg->kv_dtype == PA_DTYPE_INT8 && (!k_absmax || !v_absmax))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": int8 append needs k_absmax and v_absmax");
     const int G = cfg->num_q_heads / cfg->num_kv_heads;
     const bool g_ok = cfg->kv_dtype == PA_DTYPE_FP32 ? (G == 1 || G == 2 || G == 4 || G == 8)
                                                      : (G == 1 || G == 2 || G == 4 || G == 8 || G == 16);
-    if (!g_ok) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: unsupported Hq / Hkv ratio");
-    if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: too many KV heads");
+    if (!g_ok) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": unsupported Hq / Hkv ratio");
+    if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": too many KV heads");
 
     const int32_t max_len = effective_max_len(max_context_len, max_blocks_per_seq);
     std::string err;
     // The partition length is resolved from the caller's max_context_len, exactly as
     // pa_decode_workspace_size does, so both agree on the workspace layout.
     const int part = resolve_part(cfg, max_context_len, &err);
-    if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: " + err);
+    if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": " + err);
     const int32_t max_parts = max_len > 0 ? (max_len + part - 1) / part : 1;
     const size_t need = workspace_bytes_for(cfg, num_seqs, max_len, part);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return pa::set_error(PA_ERROR_WORKSPACE_TOO_SMALL,
-                             "pa_paged_decode: workspace of " + std::to_string(need) + " bytes required");
+                             f + ": workspace of " + std::to_string(need) + " bytes required");
 
     DecodeArgs a{};
     a.out = out;
@@ -857,6 +1062,10 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
     a.v_scale = v_scale;
     a.block_tables = block_tables;
     a.context_lens = context_lens;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k_absmax = k_absmax;
+    a.v_absmax = v_absmax;
     a.num_kv_heads = cfg->num_kv_heads;
     a.group = G;
     a.max_blocks_per_seq = max_blocks_per_seq;
@@ -877,11 +1086,11 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
     dim3 grid(max_parts, cfg->num_kv_heads, num_seqs);
     bool ok = false;
     switch (cfg->head_dim) {
-        case 64: ok = launch_decode<64>(cfg, a, grid, s); break;
-        case 128: ok = launch_decode<128>(cfg, a, grid, s); break;
-        case 256: ok = launch_decode<256>(cfg, a, grid, s); break;
+        case 64: ok = append ? launch_decode<64, true>(cfg, a, grid, s) : launch_decode<64, false>(cfg, a, grid, s); break;
+        case 128: ok = append ? launch_decode<128, true>(cfg, a, grid, s) : launch_decode<128, false>(cfg, a, grid, s); break;
+        case 256: ok = append ? launch_decode<256, true>(cfg, a, grid, s) : launch_decode<256, false>(cfg, a, grid, s); break;
     }
-    if (!ok) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_paged_decode: configuration not compiled");
+    if (!ok) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": configuration not compiled");
     PA_HIP_CHECK(hipGetLastError());
     if (max_parts > 1) {
         dim3 mgrid(cfg->num_kv_heads, num_seqs);
@@ -893,6 +1102,31 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
         PA_HIP_CHECK(hipGetLastError());
     }
     return pa::clear_error();
+}
+
+}  // namespace
+
+extern "C" {
+
+pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                          const void* k_cache, const void* v_cache, const float* k_scale,
+                          const float* v_scale, const int32_t* block_tables, const int32_t* context_lens,
+                          int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
+                          void* workspace, size_t workspace_bytes) {
+    return decode_impl("pa_paged_decode", false, stream, cfg, out, q, nullptr, nullptr, k_cache, v_cache, k_scale,
+                       v_scale, nullptr, nullptr, block_tables, context_lens, num_seqs, max_blocks_per_seq,
+                       max_context_len, workspace, workspace_bytes);
+}
+
+pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                 const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                                 float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
+                                 const int32_t* block_tables, const int32_t* context_lens, int32_t num_seqs,
+                                 int32_t max_blocks_per_seq, int32_t max_context_len, void* workspace,
+                                 size_t workspace_bytes) {
+    return decode_impl("pa_paged_decode_append", true, stream, cfg, out, q, k_new, v_new, k_cache, v_cache,
+                       k_scale, v_scale, k_absmax, v_absmax, block_tables, context_lens, num_seqs,
+                       max_blocks_per_seq, max_context_len, workspace, workspace_bytes);
 }
 
 }  // extern "C"

@@ -50,7 +50,7 @@ EXPORTS = (
     "pa_event_create", "pa_event_destroy", "pa_event_record", "pa_event_query",
     "pa_event_synchronize", "pa_event_elapsed_ms",
     "pa_build_slot_mapping", "pa_kv_append", "pa_decode_workspace_size", "pa_paged_decode",
-    "pa_chunked_prefill",
+    "pa_paged_decode_append", "pa_chunked_prefill",
 )
 
 
@@ -128,6 +128,8 @@ _SIGNATURES = {
     "pa_kv_append": [_P, _CFG, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P],
     "pa_decode_workspace_size": [_CFG, _I32, _I32, ctypes.POINTER(_SZ)],
     "pa_paged_decode": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _SZ],
+    "pa_paged_decode_append": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                               _P, _SZ],
     "pa_chunked_prefill": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
 }
 
@@ -275,6 +277,15 @@ def paged_decode(stream, cfg: PaConfig, out, q, k_cache, v_cache, k_scale, v_sca
          _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_tables),
          _ptr(context_lens), num_seqs, max_blocks_per_seq, max_context_len, _ptr(workspace),
          workspace_bytes)
+
+
+def paged_decode_append(stream, cfg: PaConfig, out, q, k_new, v_new, k_cache, v_cache, k_scale, v_scale,
+                        k_absmax, v_absmax, block_tables, context_lens, num_seqs, max_blocks_per_seq,
+                        max_context_len, workspace=None, workspace_bytes=0):
+    call("pa_paged_decode_append", stream.handle if stream else None, ctypes.byref(cfg), _ptr(out), _ptr(q),
+         _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+         _ptr(k_absmax), _ptr(v_absmax), _ptr(block_tables), _ptr(context_lens), num_seqs,
+         max_blocks_per_seq, max_context_len, _ptr(workspace), workspace_bytes)
 
 
 def chunked_prefill(stream, cfg: PaConfig, out, q, q_start_loc, prefix_lens, k_cache, v_cache,

@@ -75,10 +75,17 @@ def run_decode(w, seed, stream, partition_size=0, n_threads=NTHREADS):
     mcl = w.max_context_len
     wsb = pa.decode_workspace_size(cfg, S, mcl)
     ws = empty_gpu((max(wsb, 1),), np.uint8)
-    pa.paged_decode(stream, cfg, out, to_gpu(inp["q"]), kc, vc, ks, vs, to_gpu(w.block_tables),
-                    to_gpu(w.context_lens), S, w.max_blocks, mcl, ws, wsb)
+    args = (to_gpu(inp["q"]), kc, vc, ks, vs, to_gpu(w.block_tables), to_gpu(w.context_lens), S,
+            w.max_blocks, mcl, ws, wsb)
+    pa.paged_decode(stream, cfg, out, *args)
     _sync()
-    return to_np(out), ref
+    first = to_np(out).copy()
+    # A second call on the same (now dirty) workspace must reproduce the first bit for bit.
+    out.fill_(float("nan"))
+    pa.paged_decode(stream, cfg, out, *args)
+    _sync()
+    np.testing.assert_array_equal(to_np(out), first)
+    return first, ref
 
 
 # ---- slot mapping ----------------------------------------------------------------------------------
@@ -212,3 +219,62 @@ def test_decode_invalid_block_ids_read_as_zero(stream):
     w.block_tables[2, 10] = w.num_blocks + 5
     got, ref = run_decode(w, 56, stream)
     check_close(got, ref, **tol_for(1), what="invalid ids")
+
+
+# ---- fused append + decode ------------------------------------------------------------------------
+# Positions T-1 with (T-1) % 16 == 0 start a block (fresh int8 statistics); the rest append mid-block.
+APPEND_LENS = [1, 2, 16, 17, 33, 100, 256, 257, 300, 513, 1000, 1024, 1025, 2000]
+
+
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,part", [
+    (1, 1, 32, 8, 128, 256), (1, 0, 16, 4, 64, 512), (2, 0, 32, 8, 128, 256), (2, 1, 8, 2, 256, 512),
+    (0, 0, 8, 8, 64, 256), (0, 1, 16, 4, 128, 512),
+])
+def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part):
+    w = wl.make_small(70 + D + kv_dtype, num_seqs=len(APPEND_LENS), lens=APPEND_LENS, Hq=Hq, Hkv=Hkv, D=D,
+                      kv_dtype=kv_dtype, q_dtype=q_dtype)
+    inp = wl.numpy_inputs(w, 77)
+    cfg = config_for(w, partition_size=part)
+    S = w.num_seqs
+    rng = np.random.default_rng(78)
+    k_new = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    v_new = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    k_new[::2, :, 5] *= 8.0   # outliers: int8 scale growth for half of the sequences
+    v_new[1::3, :, 9] *= 8.0
+    if q_dtype == 1:
+        k_new, v_new = orc.bf16_from_f32(k_new), orc.bf16_from_f32(v_new)
+    pos = w.context_lens.astype(np.int64) - 1
+    slots = w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16
+
+    if kv_dtype == 2:
+        host, g = build_int8_caches(w, inp, stream)
+        ka, va = g["ka"], g["va"]
+        host_amax = (to_np(ka).copy(), to_np(va).copy())
+        kc, vc, ks, vs = g["kc"], g["vc"], g["ks"], g["vs"]
+        hk, hv = host["k_cache"].copy(), host["v_cache"].copy()
+        hks, hvs = host["k_scale"].copy(), host["v_scale"].copy()
+        orc.kv_append(cfg, k_new, v_new, slots, hk, hv, hks, hvs, host_amax[0], host_amax[1])
+    else:
+        kc, vc, ks, vs, ka, va = to_gpu(inp["k_cache"]), to_gpu(inp["v_cache"]), None, None, None, None
+        hk, hv = inp["k_cache"].copy(), inp["v_cache"].copy()
+        hks = hvs = None
+        orc.kv_append(cfg, k_new, v_new, slots, hk, hv)
+    ref = orc.paged_decode(cfg, inp["q"], hk, hv, hks, hvs, w.block_tables, w.context_lens, n_threads=NTHREADS)
+
+    out = empty_gpu((S, Hq, D), np.float32)
+    out.fill_(float("nan"))
+    mcl = w.max_context_len
+    wsb = pa.decode_workspace_size(cfg, S, mcl)
+    ws = empty_gpu((max(wsb, 1),), np.uint8)
+    pa.paged_decode_append(stream, cfg, out, to_gpu(inp["q"]), to_gpu(k_new), to_gpu(v_new), kc, vc, ks, vs, ka,
+                           va, to_gpu(w.block_tables), to_gpu(w.context_lens), S, w.max_blocks, mcl, ws, wsb)
+    _sync()
+    cdt = {0: np.float32, 1: np.uint16, 2: np.int8}[kv_dtype]
+    np.testing.assert_array_equal(to_np(kc, cdt), hk, err_msg="K cache after fused append")
+    np.testing.assert_array_equal(to_np(vc, cdt), hv, err_msg="V cache after fused append")
+    if kv_dtype == 2:
+        np.testing.assert_array_equal(to_np(ks), hks, err_msg="k_scale")
+        np.testing.assert_array_equal(to_np(vs), hvs, err_msg="v_scale")
+        np.testing.assert_array_equal(to_np(ka), host_amax[0], err_msg="k_absmax")
+        np.testing.assert_array_equal(to_np(va), host_amax[1], err_msg="v_absmax")
+    check_close(to_np(out), ref, **tol_for(kv_dtype), what=f"fused append kv={kv_dtype} q={q_dtype} D={D}")
