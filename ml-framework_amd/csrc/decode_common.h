@@ -1,0 +1,344 @@
+// decode_common.h -- shared definitions of the paged-decode kernels (argument block, helpers,
+// partition merge, fused-append register patches). Included by the decode translation units.
+#pragma once
+
+#include <string>
+
+#include "pa_internal.h"
+
+namespace pa {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct DecodeArgs {
+    float* out;
+    const void* q;
+    const void* k_cache;
+    const void* v_cache;
+    const float* k_scale;
+    const float* v_scale;
+    const int32_t* block_tables;
+    const int32_t* context_lens;
+    float* ws_o;  // [num_seqs][Hq][max_parts][D]
+    float* ws_m;  // [num_seqs][Hq][max_parts]
+    float* ws_l;  // [num_seqs][Hq][max_parts]
+    // fused append (pa_paged_decode_append): the token at position context_len - 1
+    const void* k_new;  // [num_seqs][Hkv][D] of the activation dtype
+    const void* v_new;
+    float* k_absmax;    // int8 caches: running absmax / scale per (block, KV head), updated
+    float* v_absmax;
+    int32_t num_kv_heads;
+    int32_t group;  // G = Hq / Hkv
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    int32_t max_context_len;
+    int32_t max_parts;
+    int32_t part;  // partition length in tokens (multiple of 64)
+    int32_t q_bf16;
+    float scale;
+};
+
+__device__ __forceinline__ int clamp_len(const DecodeArgs& a, int seq) {
+    int T = a.context_lens[seq];
+    T = min(T, a.max_blocks_per_seq * pa::kBlockSize);
+    T = min(T, a.max_context_len);
+    return T;
+}
+
+// Final write of one (sequence, query head, dim): normalised output, or the partition's partial.
+__device__ __forceinline__ void emit(const DecodeArgs& a, int seq, int h, int part, int nparts, int D,
+                                     int d, float o, float m, float l) {
+    const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * a.group + h;
+    if (nparts == 1) {
+        a.out[row * D + d] = o / l;
+    } else {
+        const int64_t pidx = row * a.max_parts + part;
+        a.ws_o[pidx * D + d] = o;
+        if (d == 0) {
+            a.ws_m[pidx] = m;
+            a.ws_l[pidx] = l;
+        }
+    }
+}
+
+// ================================================================================================
+// bf16 / int8 caches: MFMA kernel.
+// ================================================================================================
+template <int KV> struct MfmaRaw;
+template <> struct MfmaRaw<PA_DTYPE_BF16> {
+    using K = uint4;  // 8 bf16 of one token row (A operand of the 16x16x32 MFMA)
+    using V = uint2;  // 4 bf16: 4 consecutive tokens of one dim (B operand of the 16x16x16 MFMA)
+    static constexpr int kElt = 2;
+};
+template <> struct MfmaRaw<PA_DTYPE_INT8> {
+    using K = uint2;     // 8 int8 codes
+    using V = uint32_t;  // 4 int8 codes
+    static constexpr int kElt = 1;
+};
+
+// fp32 -> bf16 bits by truncation (the reference's conversion, BFloat16.cs:99-107).
+__device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
+    return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_i8pair(uint32_t w, int k) {
+    // Codes k and k+1 of w as two bf16 (exact: |code| <= 128 needs 8 significant bits).
+    return pack_bf16_trunc(pa::i8_at(w, k), pa::i8_at(w, k + 1));
+}
+
+// Reductions across the 4 rows of 16 lanes with gfx950's v_permlane16/32_swap (VALU, no LDS):
+// each swap returns the pair {x[l], x[l ^ 16]} (resp. x[l ^ 32]) in some order.
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Log-sum-exp merge of the partitions of one (sequence, KV head): wave w takes query heads
+// w, w + 4, ... Partition statistics are read 64 at a time (one per lane); the weighted sum over
+// partitions issues its loads in groups of 8 so their latencies overlap.
+template <int D>
+__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts) {
+    constexpr int DPL = D / 64;  // dims per lane
+    constexpr int CHUNK = 16;    // partitions whose loads are issued together
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = a.group;
+    for (int g = wave; g < G; g += 4) {
+        const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
+        const int64_t base = row * a.max_parts;
+        float M = -INFINITY, L = 0.0f;
+        float o[DPL];
+#pragma unroll
+        for (int k = 0; k < DPL; k++) o[k] = 0.0f;
+        // Running log-sum-exp over chunks of partitions; within a chunk every load (m, l and the
+        // partial outputs) is issued before any is used.
+        for (int p0 = 0; p0 < nparts; p0 += CHUNK) {
+            const int cnt = min(CHUNK, nparts - p0);
+            float pm[CHUNK], pl[CHUNK], po[CHUNK][DPL];
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) {
+                const bool ok = u < cnt;
+                const int64_t pi = base + p0 + (ok ? u : 0);
+                pm[u] = ok ? a.ws_m[pi] : -INFINITY;
+                pl[u] = ok ? a.ws_l[pi] : 0.0f;
+#pragma unroll
+                for (int k = 0; k < DPL; k++) po[u][k] = ok ? a.ws_o[pi * D + lane + 64 * k] : 0.0f;
+            }
+            float cm = M;
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) cm = fmaxf(cm, pm[u]);
+            const float r = __expf(M - cm);  // rescale of what was accumulated (0 on the first chunk)
+            L *= r;
+#pragma unroll
+            for (int k = 0; k < DPL; k++) o[k] *= r;
+#pragma unroll
+            for (int u = 0; u < CHUNK; u++) {
+                const float w = __expf(pm[u] - cm);
+                L += pl[u] * w;
+#pragma unroll
+                for (int k = 0; k < DPL; k++) o[k] += po[u][k] * w;
+            }
+            M = cm;
+        }
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
+    }
+}
+
+// Merge pass: one workgroup per (KV head, sequence).
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
+    const int kvh = blockIdx.x, seq = blockIdx.y;
+    const int T = clamp_len(a, seq);
+    if (T <= 0) return;
+    const int nparts = (T + a.part - 1) / a.part;
+    if (nparts <= 1) return;
+    merge_partitions<D>(a, seq, kvh, nparts);
+}
+
+__device__ __forceinline__ bf16x8_t k_operand(const uint4& r) { return __builtin_bit_cast(bf16x8_t, r); }
+__device__ __forceinline__ bf16x8_t k_operand(const uint2& r) {
+    const uint4 p = make_uint4(pack_i8pair(r.x, 0), pack_i8pair(r.x, 2), pack_i8pair(r.y, 0), pack_i8pair(r.y, 2));
+    return __builtin_bit_cast(bf16x8_t, p);
+}
+__device__ __forceinline__ s16x4_t v_operand(const uint2& r) { return __builtin_bit_cast(s16x4_t, r); }
+__device__ __forceinline__ s16x4_t v_operand(const uint32_t& r) {
+    const uint2 p = make_uint2(pack_i8pair(r, 0), pack_i8pair(r, 2));
+    return __builtin_bit_cast(s16x4_t, p);
+}
+
+// ---- fused append: the new token (row r of the sequence's last block) enters the owning wave's
+// registers and the cache. Values and cache bytes are those of pa_kv_append for that one token.
+__device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
+    return f32 ? static_cast<const float*>(p)[i] : pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// The new token's K values are at s_new[0, D) and its V values at s_new[D, 2D) (LDS, fp32 holding
+// the activation values). The owning wave patches row r of the tile it holds in registers and
+// writes the same bytes to the cache.
+template <int D>
+__device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t tile, const float* s_new, int r,
+                                                 int q4, int n, uint4 (&kr)[D / 32], uint2 (&vr)[D / 16]) {
+    constexpr int NSLAB = D / 32, NT = D / 16;
+    uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache));
+    uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache));
+    if (n == r) {  // K row r: dims 32s + 8q4 .. +8 of this lane
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++) {
+            const int d0 = 32 * sl + 8 * q4;
+            const float* x = s_new + d0;
+            const uint4 v = make_uint4(pack_bf16_trunc(x[0], x[1]), pack_bf16_trunc(x[2], x[3]),
+                                       pack_bf16_trunc(x[4], x[5]), pack_bf16_trunc(x[6], x[7]));
+            kr[sl] = v;
+            *reinterpret_cast<uint4*>(kc + tile + r * D + d0) = v;
+        }
+    }
+    if (q4 == (r >> 2)) {  // V column r: element r & 3 of this lane's 4-token run, dims 16t + n
+        const int e = r & 3;
+        const uint32_t sh = (e & 1) * 16;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int d = 16 * t + n;
+            const uint32_t b = __float_as_uint(s_new[D + d]) >> 16;
+            const uint32_t mask = ~(0xffffu << sh);
+            if (e < 2) vr[t].x = (vr[t].x & mask) | (b << sh);
+            else vr[t].y = (vr[t].y & mask) | (b << sh);
+            vc[tile + d * 16 + r] = static_cast<uint16_t>(b);
+        }
+    }
+}
+
+__device__ __forceinline__ int code_at(uint32_t w, int k) { return static_cast<int32_t>(w << (24 - 8 * k)) >> 24; }
+__device__ __forceinline__ uint32_t with_code(uint32_t w, int k, int8_t c) {
+    return (w & ~(0xffu << (8 * k))) | (static_cast<uint32_t>(static_cast<uint8_t>(c)) << (8 * k));
+}
+
+// Running statistics of one (block, KV head) before the append.
+struct Int8Stats {
+    float k_absmax, k_scale, v_absmax, v_scale;
+};
+
+// int8: the owning wave holds the whole (block, head) tile in registers (K: 8 codes per lane per
+// 32-dim slab, V: 4 codes per lane per 16-dim tile), so the scale growth and requantisation of
+// pa_kv_append run in place. Returns the tile's K and V scales after the append.
+template <int D>
+__device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t tile, int64_t sidx, const float* s_new,
+                                                 int r, int q4, int n, const Int8Stats& old, uint2 (&kr)[D / 32],
+                                                 uint32_t (&vr)[D / 16], float& k_scale_out, float& v_scale_out) {
+#pragma clang fp contract(off)
+    constexpr int NSLAB = D / 32, NT = D / 16;
+    int8_t* kc = static_cast<int8_t*>(const_cast<void*>(a.k_cache));
+    int8_t* vc = static_cast<int8_t*>(const_cast<void*>(a.v_cache));
+    float* kscale = const_cast<float*>(a.k_scale);
+    float* vscale = const_cast<float*>(a.v_scale);
+    const bool fresh = r == 0;  // writing row 0 starts the block afresh
+    const int lane = threadIdx.x & 63;
+    // ---------------- K ----------------
+    {
+        float x[NSLAB][8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                x[sl][e] = n == r ? s_new[32 * sl + 8 * q4 + e] : 0.0f;
+                const float ax = fabsf(x[sl][e]);
+                amax = ax > amax ? ax : amax;
+            }
+        amax = pa::wave_max(amax);
+        const float old_amax = fresh ? 0.0f : old.k_absmax;
+        const float old_scale = fresh ? 0.0f : old.k_scale;
+        const bool grow = !fresh && amax > old_amax;
+        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++) {
+            uint32_t w[2] = {kr[sl].x, kr[sl].y};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                int8_t c;
+                if (n == r) c = pa::quantize_symmetric(x[sl][e], sc);
+                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w[e >> 2], e & 3)) * old_scale, sc);
+                else c = static_cast<int8_t>(code_at(w[e >> 2], e & 3));
+                w[e >> 2] = with_code(w[e >> 2], e & 3, c);
+            }
+            kr[sl] = make_uint2(w[0], w[1]);
+            if (grow || n == r) *reinterpret_cast<uint2*>(kc + tile + n * D + 32 * sl + 8 * q4) = kr[sl];
+        }
+        if (lane == 0 && (fresh || grow)) {
+            a.k_absmax[sidx] = amax;
+            kscale[sidx] = sc;
+        }
+        k_scale_out = sc;
+    }
+    // ---------------- V (tile is [D][16]: lane holds tokens 4q4..4q4+3 of dim 16t+n) ----------------
+    {
+        const bool mine = q4 == (r >> 2);
+        const int er = r & 3;
+        float x[NT];
+        float amax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            x[t] = mine ? s_new[D + 16 * t + n] : 0.0f;
+            const float ax = fabsf(x[t]);
+            amax = ax > amax ? ax : amax;
+        }
+        amax = pa::wave_max(amax);
+        const float old_amax = fresh ? 0.0f : old.v_absmax;
+        const float old_scale = fresh ? 0.0f : old.v_scale;
+        const bool grow = !fresh && amax > old_amax;
+        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            uint32_t w = vr[t];
+            int8_t newc = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool is_new = mine && e == er;
+                int8_t c;
+                if (is_new) c = newc = pa::quantize_symmetric(x[t], sc);
+                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w, e)) * old_scale, sc);
+                else c = static_cast<int8_t>(code_at(w, e));
+                w = with_code(w, e, c);
+            }
+            vr[t] = w;
+            int8_t* dst = vc + tile + (16 * t + n) * 16;
+            if (grow) *reinterpret_cast<uint32_t*>(dst + 4 * q4) = w;
+            else if (mine) dst[r] = newc;
+        }
+        if (lane == 0 && (fresh || grow)) {
+            a.v_absmax[sidx] = amax;
+            vscale[sidx] = sc;
+        }
+        v_scale_out = sc;
+    }
+}
+
+// ---- launchers (one translation unit per kernel family) ----------------------------------------
+constexpr int kMaxPersistentSeqs = 2048;  // per-sequence tables of the persistent kernel (LDS)
+int device_cus();
+// bf16 / int8 caches; num_seqs < kMaxPersistentSeqs; max_items bounds the useful grid.
+void launch_decode_mfma_d64(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+                            int64_t max_items, hipStream_t s);
+void launch_decode_mfma_d128(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+                             int64_t max_items, hipStream_t s);
+void launch_decode_mfma_d256(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+                             int64_t max_items, hipStream_t s);
+// fp32 caches: grid (max_parts, Hkv, num_seqs); returns false for an uncompiled shape.
+bool launch_decode_fp32(const DecodeArgs& a, int head_dim, dim3 grid, hipStream_t s);
+
+}  // namespace pa

@@ -1,0 +1,41 @@
+// decode_mfma_d256.hip -- instantiations of the MFMA paged-decode kernel for head_dim 256.
+#include "decode_mfma.h"
+
+namespace pa {
+namespace {
+
+template <int D, int KV, bool QF32, bool APPEND>
+void launch_one(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t s) {
+    auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND>;
+    // Resident workgroups per CU for this instance (queried once; read-only afterwards).
+    static const int per_cu = [&] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, 0) != hipSuccess || n < 1) n = 1;
+        return n;
+    }();
+    int64_t nwg = static_cast<int64_t>(device_cus()) * per_cu;
+    if (nwg > max_items) nwg = max_items;
+    if (nwg < 1) nwg = 1;
+    kern<<<static_cast<unsigned>(nwg), 256, 0, s>>>(a, num_seqs);
+}
+
+template <int KV, bool QF32>
+void pick_append(const DecodeArgs& a, bool append, int num_seqs, int64_t max_items, hipStream_t s) {
+    if (append) launch_one<256, KV, QF32, true>(a, num_seqs, max_items, s);
+    else launch_one<256, KV, QF32, false>(a, num_seqs, max_items, s);
+}
+
+}  // namespace
+
+void launch_decode_mfma_d256(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+                            int64_t max_items, hipStream_t s) {
+    if (kv_dtype == PA_DTYPE_BF16) {
+        if (q_f32) pick_append<PA_DTYPE_BF16, true>(a, append, num_seqs, max_items, s);
+        else pick_append<PA_DTYPE_BF16, false>(a, append, num_seqs, max_items, s);
+    } else {
+        if (q_f32) pick_append<PA_DTYPE_INT8, true>(a, append, num_seqs, max_items, s);
+        else pick_append<PA_DTYPE_INT8, false>(a, append, num_seqs, max_items, s);
+    }
+}
+
+}  // namespace pa
