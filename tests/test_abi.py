@@ -1,0 +1,139 @@
+"""The C-ABI of libpa_hip.so on a machine without a GPU: the library loads, exports every function
+include/paged_attn.h declares, and its host-side validation returns the documented status codes
+before anything is launched (no call here reaches a kernel launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import paged_attention as pa
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "paged_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:pa_status|const char\*)\s+(pa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = pa.load_library()
+    names = declared_functions()
+    assert len(names) >= 30
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in paged_attn.h but not exported"
+    assert sorted(pa.EXPORTS) == names, "binding's export list differs from the header"
+
+
+def test_version_and_status_strings():
+    lib = pa.load_library()
+    major, minor = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.pa_get_version(ctypes.byref(major), ctypes.byref(minor)) == 0
+    assert (major.value, minor.value) == (1, 0)
+    for code, name in [(0, b"PA_SUCCESS"), (1, b"PA_ERROR_INVALID_ARGUMENT"), (2, b"PA_ERROR_INVALID_CONFIG"),
+                       (3, b"PA_ERROR_OUT_OF_MEMORY"), (4, b"PA_ERROR_HIP"), (5, b"PA_ERROR_UNSUPPORTED"),
+                       (6, b"PA_ERROR_WORKSPACE_TOO_SMALL"), (7, b"PA_ERROR_NO_DEVICE")]:
+        assert lib.pa_status_string(code) == name
+    assert lib.pa_status_string(99) == b"PA_ERROR_UNKNOWN"
+
+
+def cfg(**kw):
+    base = dict(num_q_heads=32, num_kv_heads=8, head_dim=128, kv_dtype=pa.PA_DTYPE_BF16,
+                q_dtype=pa.PA_DTYPE_BF16, num_blocks=100)
+    base.update(kw)
+    return pa.make_config(**base)
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("c,status,msg", [
+    (cfg(block_size=32), pa.PA_ERROR_UNSUPPORTED, "block_size"),
+    (cfg(num_q_heads=12), pa.PA_ERROR_INVALID_CONFIG, "multiple"),
+    (cfg(head_dim=96), pa.PA_ERROR_UNSUPPORTED, "head_dim"),
+    (cfg(kv_dtype=7), pa.PA_ERROR_UNSUPPORTED, "kv_dtype"),
+    (cfg(q_dtype=pa.PA_DTYPE_INT8), pa.PA_ERROR_UNSUPPORTED, "q_dtype"),
+    (cfg(num_blocks=-1), pa.PA_ERROR_INVALID_CONFIG, "num_blocks"),
+    (cfg(scale=float("nan")), pa.PA_ERROR_INVALID_CONFIG, "scale"),
+])
+def test_config_validation(c, status, msg):
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.paged_decode(None, c, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
+    assert e.value.status == status and msg in str(e.value)
+
+
+def test_argument_validation():
+    c = cfg()
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.call("pa_paged_decode", None, None, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 1, 1, 1, None, 0)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.paged_decode(None, c, None, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.paged_decode(None, c, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, -1, 10, 100)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:  # int8 without scales
+        pa.paged_decode(None, cfg(kv_dtype=2), FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:  # Hq / Hkv = 3
+        pa.paged_decode(None, cfg(num_q_heads=24), FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
+    assert e.value.status == pa.PA_ERROR_UNSUPPORTED
+    with pytest.raises(pa.PagedAttentionError) as e:  # long contexts need a workspace
+        pa.paged_decode(None, c, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 300, 4096, None, 0)
+    assert e.value.status == pa.PA_ERROR_WORKSPACE_TOO_SMALL
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.paged_decode_append(None, c, FAKE, FAKE, None, FAKE, FAKE, FAKE, None, None, None, None, FAKE, FAKE,
+                               4, 10, 100)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:  # int8 append without running absmax
+        pa.paged_decode_append(None, cfg(kv_dtype=2), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None,
+                               FAKE, FAKE, 4, 10, 100)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.kv_append(None, c, FAKE, FAKE, FAKE, -3, FAKE, FAKE)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.kv_append(None, cfg(kv_dtype=2), FAKE, FAKE, FAKE, 5, FAKE, FAKE)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.build_slot_mapping(None, cfg(block_size=8), FAKE, 4, FAKE, FAKE, FAKE, 2, 3, FAKE)
+    assert e.value.status == pa.PA_ERROR_UNSUPPORTED
+    # empty batches are no-ops that succeed without touching any pointer
+    pa.paged_decode(None, c, None, None, None, None, None, None, None, None, 0, 0, 0)
+    pa.kv_append(None, c, None, None, None, 0, None, None)
+
+
+def test_workspace_size():
+    c = cfg()
+    # one partition per sequence: no workspace
+    assert pa.decode_workspace_size(c, 64, 256) == 0
+    # default partition for max_len 4096 is 256 -> 16 partitions of (D + 2) floats per query head
+    assert pa.decode_workspace_size(c, 64, 4096) == 64 * 32 * 16 * (128 + 2) * 4
+    # 1/16 of the longest context, rounded up to 256 tokens: 32768 -> 2048 -> 16 partitions
+    assert pa.decode_workspace_size(c, 8, 32768) == 8 * 32 * 16 * 130 * 4
+    assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 64 * 32 * 8 * 130 * 4
+    assert pa.decode_workspace_size(cfg(kv_dtype=0), 4, 256) == 0
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.decode_workspace_size(cfg(partition_size=100), 4, 256)
+    assert e.value.status == pa.PA_ERROR_UNSUPPORTED
+    with pytest.raises(pa.PagedAttentionError):
+        pa.decode_workspace_size(cfg(kv_dtype=0, partition_size=1024), 4, 256)
+
+
+def test_last_error_is_per_call():
+    with pytest.raises(pa.PagedAttentionError):
+        pa.paged_decode(None, cfg(head_dim=48), FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
+    assert "head_dim" in pa.last_error()
+    assert pa.decode_workspace_size(cfg(), 1, 16) == 0
+    assert pa.last_error() == ""
+
+
+def test_device_open_without_gpu_reports_no_device():
+    n = ctypes.c_int32(-1)
+    assert pa.load_library().pa_device_count(ctypes.byref(n)) == 0
+    if n.value == 0:
+        with pytest.raises(pa.PagedAttentionError) as e:
+            pa.Device(0)
+        assert e.value.status == pa.PA_ERROR_NO_DEVICE
