@@ -255,7 +255,7 @@ def main():
             "num_seqs": S, "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
             "head_dim": w.head_dim, "block_size": 16, "context_lens": "log-uniform [128, 4096]",
             "context_tokens": int(w.context_lens.sum()), "num_blocks": w.num_blocks,
-            "partition_size": args.partition_size or 256, "parallelism": "single GPU",
+            "partition_size": args.partition_size or "library default", "parallelism": "single GPU",
         },
         "pct_peak_hbm": round(100.0 * value / PEAK_HBM_GBPS, 2),
         "tokens_per_s_per_layer": round(S / (step_ms * 1e-3), 1),

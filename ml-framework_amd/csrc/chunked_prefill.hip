@@ -1,17 +1,328 @@
-// chunked_prefill.hip -- chunked prefill (bf16 MFMA). Not yet implemented: returns
-// PA_ERROR_UNSUPPORTED after validating its arguments.
-#include "pa_internal.h"
+// chunked_prefill.hip -- chunked prefill over the paged cache on gfx950 MFMA.
+//
+// Computes, for each prefill sequence s, attention of its chunk's queries (positions
+// prefix_lens[s] + i) over keys [0, prefix_lens[s] + chunk_len) read through the block table --
+// the reference's StandardPagedAttentionKernel (Kernels/StandardPagedAttentionKernel.cs:21-84)
+// called with phase Decode on the gathered prefix + chunk, whose mask is bottom-right aligned
+// (:57-66, :219-255). The reference splits long prompts into 512-token chunks on the host
+// (ContinuousBatching/Prefill/PrefillHandler.cs:85-89, PrefillConfiguration.cs:21); each chunk is
+// one call here.
+//
+// Work decomposition: one workgroup per (16-query tile, KV head, sequence); wave w handles query
+// head w (w + 4, ...) of the KV head's group, so the group's 4 waves read the same K/V tiles
+// (HBM once, L1/L2 after). Per 16-key block: S^T[16 keys][16 queries] = K . Q^T on
+// v_mfma_f32_16x16x32_bf16, online softmax per query in fp32 with the causal limit per query,
+// O[16 queries][D] += P . V on v_mfma_f32_16x16x16_bf16 with P split into bf16 high and low parts.
+// These are the decode kernel's operand layouts with the 16 MFMA rows holding 16 queries instead
+// of (padded) heads.
+#include <string>
 
-extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out,
-                                        const void* q, const int32_t* q_start_loc,
-                                        const int32_t* prefix_lens, const void* k_cache,
-                                        const void* v_cache, const float* k_scale, const float* v_scale,
-                                        const int32_t* block_tables, int32_t num_seqs,
+#include "decode_common.h"
+
+namespace pa {
+namespace {
+
+struct PrefillArgs {
+    float* out;
+    const void* q;
+    const void* k_cache;
+    const void* v_cache;
+    const float* k_scale;
+    const float* v_scale;
+    const int32_t* q_start_loc;
+    const int32_t* prefix_lens;
+    const int32_t* block_tables;
+    int32_t num_kv_heads;
+    int32_t group;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    int32_t mask_mode;  // 0 causal, 1 causal only when the prefix is non-empty, 2 no mask
+    float scale;
+};
+
+constexpr float kPrefillRescaleThreshold = 8.0f;
+
+template <int D, int KV, bool QF32>
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(const PrefillArgs a) {
+    using Raw = MfmaRaw<KV>;
+    constexpr int ELT = Raw::kElt;
+    constexpr int NSLAB = D / 32;
+    constexpr int NT = D / 16;
+    constexpr int TILE = 16 * D;
+    using KR = typename Raw::K;
+    using VR = typename Raw::V;
+
+    const int qt = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q4 = lane >> 4, n = lane & 15;
+    const int G = a.group, Hkv = a.num_kv_heads, Hq = Hkv * G;
+
+    const int q0 = a.q_start_loc[seq];
+    const int Lc = a.q_start_loc[seq + 1] - q0;
+    const int P = max(a.prefix_lens[seq], 0);
+    const int i0 = qt * 16;
+    if (i0 >= Lc) return;
+    const int nq = min(16, Lc - i0);
+    int T = P + Lc;
+    T = min(T, a.max_blocks_per_seq * 16);
+    const bool causal = a.mask_mode == 0 || (a.mask_mode == 1 && P > 0);
+    const int kmax = causal ? min(T, P + i0 + nq) : T;  // keys any query of the tile may see
+    const int nkb = (kmax + 15) / 16;
+    // this lane's query (column n of S^T) sees keys [0, klim)
+    const bool qvalid = n < nq;
+    const int klim = causal ? min(T, P + i0 + n + 1) : T;
+
+    const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
+    const char* kc = static_cast<const char*>(a.k_cache);
+    const char* vc = static_cast<const char*>(a.v_cache);
+    const int k_lane_off = (n * D + 8 * q4) * ELT;
+    const int v_lane_off = (n * 16 + 4 * q4) * ELT;
+
+    for (int g = wave; g < G; g += 4) {
+        const int head = kvh * G + g;
+        // Q^T operand: lane (q4, n) holds query i0 + n of this head, dims 32s + 8q4 .. +8.
+        bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
+        {
+            const int64_t qrow = (static_cast<int64_t>(q0 + i0 + (qvalid ? n : 0)) * Hq + head) * D;
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) {
+                const int d0 = 32 * s + 8 * q4;
+                if constexpr (QF32) {
+                    const float* qp = static_cast<const float*>(a.q) + qrow + d0;
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[e] = qvalid ? qp[e] : 0.0f;
+                    uint32_t h[4], l[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        h[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
+                        const float r0 = x[2 * e] - __uint_as_float(__float_as_uint(x[2 * e]) & 0xffff0000u);
+                        const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
+                        l[e] = pack_bf16_trunc(r0, r1);
+                    }
+                    qhi[s] = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+                    qlo[s] = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+                } else {
+                    const uint4 raw = qvalid
+                        ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
+                        : make_uint4(0, 0, 0, 0);
+                    qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
+                }
+            }
+        }
+
+        // Block ids (and int8 scales), 64 at a time: lane j holds key block c0 + j.
+        int bid_chunk = -1, c0 = -64;
+        float ks_chunk = 0.0f, vs_chunk = 0.0f;
+        auto refresh = [&](int lb) {
+            c0 = lb & ~63;
+            const int lbj = c0 + lane;
+            int id = -1;
+            if (lbj < nkb) {
+                id = table[lbj];
+                if (id >= a.num_blocks) id = -1;
+            }
+            bid_chunk = id;
+            if constexpr (KV == PA_DTYPE_INT8) {
+                ks_chunk = id >= 0 ? a.k_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
+                vs_chunk = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
+            }
+        };
+        auto block_id = [&](int lb) -> int {
+            if (lb >= nkb) return -1;
+            if ((lb & ~63) != c0) refresh(lb);
+            return __builtin_amdgcn_readlane(bid_chunk, lb & 63);
+        };
+        // the int8 scales of block lb are taken here, with its id: the 2-block look-ahead may
+        // move the 64-block window before block lb is consumed
+        auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], float (&kvs)[2], int lb) {
+            const int bid = block_id(lb);
+            if constexpr (KV == PA_DTYPE_INT8) {
+                kvs[0] = readlane_f(ks_chunk, lb & 63);
+                kvs[1] = readlane_f(vs_chunk, lb & 63);
+            }
+            const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
+            const int bytes = bid >= 0 ? TILE * ELT : 0;
+            const __amdgpu_buffer_rsrc_t rk =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t rv =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR>(rk, k_lane_off + 32 * s * ELT);
+#pragma unroll
+            for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
+        };
+
+        float m_run = -INFINITY, l_run = 0.0f;
+        f32x4_t acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+        auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], const float (&kvs)[2], int lb) {
+            f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int sl = 0; sl < NSLAB; sl++) {
+                const bf16x8_t kop = k_operand(kr[sl]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
+                if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+            }
+            float ks = 1.0f, vfac = 1.0f;
+            if constexpr (KV == PA_DTYPE_INT8) {
+                ks = kvs[0];
+                vfac = kvs[1];
+            }
+            const int kbase = lb * 16 + 4 * q4;
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = s[i];
+                if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
+                v = v * a.scale;
+                // queries past the tile keep finite scores (their rows are never stored)
+                sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
+            }
+            const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+            const bool grow = bm > m_run + kPrefillRescaleThreshold;
+            if (__any(grow)) {
+                const float m_new = grow ? bm : m_run;
+                const float alpha = __expf(m_run - m_new);
+                l_run *= alpha;
+                m_run = m_new;
+                float ar[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][i] *= ar[i];
+            }
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = __expf(sc[i] - m_run);
+                l_run += p[i];
+                if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
+            }
+            uint32_t hi[2], lo[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float a0 = p[2 * e], a1 = p[2 * e + 1];
+                const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+                const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+                hi[e] = pack_bf16_trunc(a0, a1);
+                lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+            }
+            const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+            const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const s16x4_t vop = v_operand(vr[t]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+            }
+        };
+
+        {
+            KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
+            VR va[NT], vb[NT], vx[NT];
+            float sa[2] = {1.0f, 1.0f}, sb[2] = {1.0f, 1.0f}, sx[2] = {1.0f, 1.0f};
+            int j = 0;
+            load(ka, va, sa, 0);
+            load(kb, vb, sb, 1);
+            while (j < nkb) {
+                load(kx, vx, sx, j + 2);
+                compute(ka, va, sa, j);
+                if (++j >= nkb) break;
+                load(ka, va, sa, j + 2);
+                compute(kb, vb, sb, j);
+                if (++j >= nkb) break;
+                load(kb, vb, sb, j + 2);
+                compute(kx, vx, sx, j);
+                ++j;
+            }
+        }
+
+        // rows of acc are queries 4q4 + i; their sums live in lanes (any q4, n = 4q4 + i)
+        const float l_tot = rows_sum(l_run);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qi = 4 * q4 + i;
+            const float li = __shfl(l_tot, qi, 64);
+            if (qi < nq) {
+                const float inv = 1.0f / li;
+                float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
+#pragma unroll
+                for (int t = 0; t < NT; t++) o[16 * t + n] = acc[t][i] * inv;
+            }
+        }
+    }
+}
+
+template <int D, int KV>
+void launch(const PrefillArgs& a, bool qf32, dim3 grid, hipStream_t s) {
+    if (qf32) chunked_prefill_kernel<D, KV, true><<<grid, 256, 0, s>>>(a);
+    else chunked_prefill_kernel<D, KV, false><<<grid, 256, 0, s>>>(a);
+}
+
+template <int D>
+void launch_kv(const PrefillArgs& a, int kv, bool qf32, dim3 grid, hipStream_t s) {
+    if (kv == PA_DTYPE_BF16) launch<D, PA_DTYPE_BF16>(a, qf32, grid, s);
+    else launch<D, PA_DTYPE_INT8>(a, qf32, grid, s);
+}
+
+}  // namespace
+}  // namespace pa
+
+extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                        const int32_t* q_start_loc, const int32_t* prefix_lens,
+                                        const void* k_cache, const void* v_cache, const float* k_scale,
+                                        const float* v_scale, const int32_t* block_tables, int32_t num_seqs,
                                         int32_t max_blocks_per_seq, int32_t max_chunk_len) {
-    (void)stream; (void)out; (void)q; (void)q_start_loc; (void)prefix_lens; (void)k_cache;
-    (void)v_cache; (void)k_scale; (void)v_scale; (void)block_tables; (void)num_seqs;
-    (void)max_blocks_per_seq; (void)max_chunk_len;
     pa_status st = pa::check_config(cfg, "pa_chunked_prefill");
     if (st != PA_SUCCESS) return st;
-    return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: not implemented yet");
+    if (num_seqs < 0 || max_blocks_per_seq < 0 || max_chunk_len < 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: negative size");
+    if (num_seqs == 0 || max_chunk_len == 0) return pa::clear_error();
+    if (num_seqs > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: num_seqs > 65535");
+    if (max_blocks_per_seq == 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: chunks need at least one block per sequence");
+    if (!out || !q || !q_start_loc || !prefix_lens || !k_cache || !v_cache || !block_tables)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: null pointer");
+    if (cfg->kv_dtype == PA_DTYPE_FP32)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: the cache must be BF16 or INT8");
+    if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: int8 cache needs k_scale and v_scale");
+    if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: too many KV heads");
+    const uint32_t masks = cfg->flags & (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK);
+    if (masks == (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK))
+        return pa::set_error(PA_ERROR_INVALID_CONFIG, "pa_chunked_prefill: conflicting mask flags");
+
+    pa::PrefillArgs a{};
+    a.out = out;
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.q_start_loc = q_start_loc;
+    a.prefix_lens = prefix_lens;
+    a.block_tables = block_tables;
+    a.num_kv_heads = cfg->num_kv_heads;
+    a.group = cfg->num_q_heads / cfg->num_kv_heads;
+    a.max_blocks_per_seq = max_blocks_per_seq;
+    a.num_blocks = cfg->num_blocks;
+    a.mask_mode = (cfg->flags & PA_FLAG_NO_MASK) ? 2 : ((cfg->flags & PA_FLAG_REFERENCE_LITERAL_MASK) ? 1 : 0);
+    a.scale = pa::resolve_scale(cfg);
+
+    dim3 grid((max_chunk_len + 15) / 16, cfg->num_kv_heads, num_seqs);
+    hipStream_t s = pa::native(stream);
+    const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
+    switch (cfg->head_dim) {
+        case 64: pa::launch_kv<64>(a, cfg->kv_dtype, qf32, grid, s); break;
+        case 128: pa::launch_kv<128>(a, cfg->kv_dtype, qf32, grid, s); break;
+        default: pa::launch_kv<256>(a, cfg->kv_dtype, qf32, grid, s); break;
+    }
+    PA_HIP_CHECK(hipGetLastError());
+    return pa::clear_error();
 }

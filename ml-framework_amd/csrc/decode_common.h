@@ -328,6 +328,20 @@ __device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t ti
     }
 }
 
+// Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
+constexpr int kBufferFlags = 0x00020000;
+
+template <typename T> __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, int off);
+template <> __device__ __forceinline__ uint4 buffer_load<uint4>(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ uint2 buffer_load<uint2>(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ uint32_t buffer_load<uint32_t>(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 // ---- launchers (one translation unit per kernel family) ----------------------------------------
 constexpr int kMaxPersistentSeqs = 2048;  // per-sequence tables of the persistent kernel (LDS)
 int device_cus();

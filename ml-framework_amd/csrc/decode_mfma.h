@@ -22,20 +22,6 @@ namespace pa {
 // while the O accumulators are rescaled on few blocks instead of on most of them.
 constexpr float kRescaleThreshold = 8.0f;
 
-// Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
-constexpr int kBufferFlags = 0x00020000;
-
-template <typename T> __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, int off);
-template <> __device__ __forceinline__ uint4 buffer_load<uint4>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-template <> __device__ __forceinline__ uint2 buffer_load<uint2>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-}
-template <> __device__ __forceinline__ uint32_t buffer_load<uint32_t>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-
 struct MfmaShared {
     float m[4][16];
     float l[4][16];
@@ -372,7 +358,7 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
 // (sequence s owns items pref[s]*Hkv .. pref[s+1]*Hkv - 1, KV head fastest), item w, w + grid, ...
 // Every workgroup leaves its loop after a bounded number of items.
 template <int D, int KV, bool QF32, bool APPEND>
-__global__ __launch_bounds__(256, 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a, int32_t num_seqs) {
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a, int32_t num_seqs) {
     __shared__ MfmaShared sh;
     __shared__ float s_x[2][D][16];
     const int tid = threadIdx.x;

@@ -50,8 +50,10 @@ using pa::act_at;
 constexpr int kMaxPart = 4096;  // a wave's block ids must fit one VGPR (64 lanes x 4 waves x 16)
 
 // Partition length for this call. fp32 caches use 256 or 512 (VALU kernel templates); bf16/int8
-// take any multiple of 64 up to 4096, defaulting to about 1/16 of the longest context (at least
-// 256), which keeps the partial count per sequence at or under 16.
+// take any multiple of 64 up to 4096. The default is about a fifth of the longest context, rounded
+// up to 256 and clamped to [256, 2048]: long enough that a partition's fixed costs (its first
+// block loads, the four-wave combine, the partial write) stay small next to its streaming time,
+// short enough that long sequences split into several work items for load balance.
 int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
     const int req = cfg->partition_size;
     if (cfg->kv_dtype == PA_DTYPE_FP32) {
@@ -61,9 +63,9 @@ int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
         return -1;
     }
     if (req == 0) {
-        int p = (max_len + 15) / 16;
+        int p = (max_len + 4) / 5;
         p = (p + 255) / 256 * 256;
-        return p < 256 ? 256 : (p > kMaxPart ? kMaxPart : p);
+        return p < 256 ? 256 : (p > 2048 ? 2048 : p);
     }
     if (req < 64 || req > kMaxPart || req % 64 != 0) {
         *err = "partition_size must be a multiple of 64 in [64, 4096]";
@@ -72,7 +74,6 @@ int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
     return req;
 }
 
-// Workspace: [o fp32 rows*D][m fp32 rows][l fp32 rows] with rows = num_seqs * Hq * max_parts.
 size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
     const int64_t max_parts = (static_cast<int64_t>(max_len) + part - 1) / part;
     if (max_parts <= 1 || num_seqs <= 0) return 0;

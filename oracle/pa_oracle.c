@@ -431,12 +431,9 @@ int orc_chunked_prefill(const pa_config* cfg, float* out, const void* q,
     const int literal = (cfg->flags & PA_FLAG_REFERENCE_LITERAL_MASK) != 0;
     const int no_mask = (cfg->flags & PA_FLAG_NO_MASK) != 0;
     int err = 0;
-#ifdef _OPENMP
     if (n_threads < 1) n_threads = 1;
-#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads) reduction(| : err)
-#else
-    (void)n_threads;
-#endif
+    /* Sequences one after another; the heads of a sequence are independent problems (the
+     * reference loops over them inside one call, :29-49), so they run in parallel. */
     for (int32_t s = 0; s < num_seqs; s++) {
         int32_t L = q_start_loc[s + 1] - q_start_loc[s];
         int32_t P = prefix_lens[s];
@@ -444,19 +441,39 @@ int orc_chunked_prefill(const pa_config* cfg, float* out, const void* q,
         if (L <= 0) continue;
         float* o = out + (size_t)q_start_loc[s] * Hq * D;
         if (P < 0 || T > max_blocks_per_seq * cfg->block_size) { err |= 1; continue; }
-        float* qs = (float*)malloc(sizeof(float) * (size_t)L * Hq * D);
         float* ks = (float*)malloc(sizeof(float) * (size_t)T * Hq * D);
         float* vs = (float*)malloc(sizeof(float) * (size_t)T * Hq * D);
-        if (!qs || !ks || !vs) { free(qs); free(ks); free(vs); err |= 1; continue; }
-        for (size_t i = 0; i < (size_t)L * Hq * D; i++)
-            qs[i] = orc_load_act(q, cfg->q_dtype, (size_t)q_start_loc[s] * Hq * D + i);
+        if (!ks || !vs) { free(ks); free(vs); err |= 1; continue; }
         const int32_t* table = block_tables + (size_t)s * max_blocks_per_seq;
         orc_gather(cfg, 0, k_cache, k_scale, table, max_blocks_per_seq, T, ks);
         orc_gather(cfg, 1, v_cache, v_scale, table, max_blocks_per_seq, T, vs);
-        int phase = no_mask ? PA_PHASE_PREFILL : PA_PHASE_DECODE;
-        int force = (!no_mask && !literal) ? 1 : 0;
-        err |= orc_sdpa(qs, ks, vs, o, 1, L, T, Hq, D, phase, cfg->scale, force) != 0;
-        free(qs); free(ks); free(vs);
+        const int phase = no_mask ? PA_PHASE_PREFILL : PA_PHASE_DECODE;
+        const int force = (!no_mask && !literal) ? 1 : 0;
+        const size_t q_base = (size_t)q_start_loc[s] * Hq * D;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads) reduction(| : err)
+#else
+        (void)n_threads;
+#endif
+        for (int32_t h = 0; h < Hq; h++) {
+            float* qh = (float*)malloc(sizeof(float) * (size_t)L * D);
+            float* kh = (float*)malloc(sizeof(float) * (size_t)T * D);
+            float* vh = (float*)malloc(sizeof(float) * (size_t)T * D);
+            float* oh = (float*)malloc(sizeof(float) * (size_t)L * D);
+            if (!qh || !kh || !vh || !oh) { free(qh); free(kh); free(vh); free(oh); err |= 1; continue; }
+            for (int32_t i = 0; i < L; i++)
+                for (int32_t d = 0; d < D; d++)
+                    qh[(size_t)i * D + d] = orc_load_act(q, cfg->q_dtype, q_base + ((size_t)i * Hq + h) * D + d);
+            for (int32_t t = 0; t < T; t++) {
+                memcpy(kh + (size_t)t * D, ks + ((size_t)t * Hq + h) * D, sizeof(float) * (size_t)D);
+                memcpy(vh + (size_t)t * D, vs + ((size_t)t * Hq + h) * D, sizeof(float) * (size_t)D);
+            }
+            err |= orc_sdpa(qh, kh, vh, oh, 1, L, T, 1, D, phase, cfg->scale, force) != 0;
+            for (int32_t i = 0; i < L; i++)
+                memcpy(o + ((size_t)i * Hq + h) * D, oh + (size_t)i * D, sizeof(float) * (size_t)D);
+            free(qh); free(kh); free(vh); free(oh);
+        }
+        free(ks); free(vs);
     }
     return err ? -1 : 0;
 }

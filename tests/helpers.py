@@ -5,6 +5,7 @@ from __future__ import annotations
 import numpy as np
 
 import paged_attention as pa
+import pa_oracle as orc
 
 BLOCK = 16
 
@@ -83,3 +84,27 @@ def pool_tokens(src: np.ndarray) -> np.ndarray:
 def config_for(w, **kw):
     return pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
                           kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks, **kw)
+
+
+def build_int8_caches(w, inp, stream):
+    """Quantises the fp32 source pool with the oracle and with the GPU append; they must agree."""
+    import torch
+
+    cfg = config_for(w)
+    nb, hkv, d = w.num_blocks, w.num_kv_heads, w.head_dim
+    slots = full_pool_slots(nb)
+    k_tok, v_tok = pool_tokens(inp["k_src"]), pool_tokens(inp["v_src"])
+    if w.q_dtype == 1:
+        k_tok, v_tok = orc.bf16_from_f32(k_tok), orc.bf16_from_f32(v_tok)
+    kc = np.zeros((nb, hkv, 16, d), np.int8)
+    vc = np.zeros_like(kc)
+    ks, vs, ka, va = (np.zeros((nb, hkv), np.float32) for _ in range(4))
+    orc.kv_append(cfg, k_tok, v_tok, slots, kc, vc, ks, vs, ka, va)
+    g = {n: empty_gpu(a.shape, a.dtype) for n, a in
+         dict(kc=kc, vc=vc, ks=ks, vs=vs, ka=ka, va=va).items()}
+    gk, gv, gsl = to_gpu(k_tok), to_gpu(v_tok), to_gpu(slots)
+    pa.kv_append(stream, cfg, gk, gv, gsl, len(slots), g["kc"], g["vc"], g["ks"], g["vs"], g["ka"], g["va"])
+    torch.cuda.synchronize()
+    for n, a in dict(kc=kc, vc=vc, ks=ks, vs=vs, ka=ka, va=va).items():
+        np.testing.assert_array_equal(to_np(g[n]), a, err_msg=f"int8 pool build: {n} differs")
+    return dict(k_cache=kc, v_cache=vc, k_scale=ks, v_scale=vs), g

@@ -109,10 +109,12 @@ def test_workspace_size():
     c = cfg()
     # one partition per sequence: no workspace
     assert pa.decode_workspace_size(c, 64, 256) == 0
-    # default partition for max_len 4096 is 256 -> 16 partitions of (D + 2) floats per query head
-    assert pa.decode_workspace_size(c, 64, 4096) == 64 * 32 * 16 * (128 + 2) * 4
-    # 1/16 of the longest context, rounded up to 256 tokens: 32768 -> 2048 -> 16 partitions
+    # default partition: a fifth of the longest context rounded up to 256, within [256, 2048]:
+    # 4096 -> 1024 -> 4 partitions of (D + 2) floats per query head
+    assert pa.decode_workspace_size(c, 64, 4096) == 64 * 32 * 4 * (128 + 2) * 4
+    # 32768 -> 2048 (clamped) -> 16 partitions
     assert pa.decode_workspace_size(c, 8, 32768) == 8 * 32 * 16 * 130 * 4
+    assert pa.decode_workspace_size(c, 64, 1000) == 64 * 32 * 4 * 130 * 4  # 1000 -> 256 -> 4 parts
     assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 64 * 32 * 8 * 130 * 4
     assert pa.decode_workspace_size(cfg(kv_dtype=0), 4, 256) == 0
     with pytest.raises(pa.PagedAttentionError) as e:

@@ -58,3 +58,17 @@ def test_int8_append_trace_matches_fixture(stream):
     for name, t in (("k_codes", kc), ("v_codes", vc), ("k_scale", ks), ("v_scale", vs), ("k_absmax", ka),
                     ("v_absmax", va)):
         np.testing.assert_array_equal(to_np(t), stored[name], err_msg=name)
+
+
+def test_prefill_matches_fixture(stream):
+    import torch
+
+    stored = np.load(os.path.join(GOLDEN, "prefill_chunk.npz"))
+    w, inp, q, q_start, prefix = cases.prefill_inputs()
+    cfg = cases.cfg_for(w)
+    out = empty_gpu(stored["out"].shape, np.float32)
+    pa.chunked_prefill(stream, cfg, out, to_gpu(q), to_gpu(q_start), to_gpu(prefix), to_gpu(inp["k_cache"]),
+                       to_gpu(inp["v_cache"]), None, None, to_gpu(w.block_tables), len(prefix), w.max_blocks,
+                       int(np.diff(q_start).max()))
+    torch.cuda.synchronize()
+    check_close(to_np(out), stored["out"], **tol_for(w.kv_dtype), what="prefill_chunk")
