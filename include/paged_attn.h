@@ -86,7 +86,10 @@ typedef struct pa_config {
                                append skips their slots)                                        */
     float   scale;          /* softmax scale; <= 0 selects 1/sqrtf(head_dim)
                                (StandardPagedAttentionKernel.cs:18,28)                          */
-    int32_t partition_size; /* decode split-K partition length in tokens; 0 = library default  */
+    int32_t partition_size; /* decode split-K granularity in tokens; 0 = library default: the
+                               batch's blocks are cut into one equal range per resident
+                               workgroup (bf16/int8) or 256-token partitions (fp32). Otherwise a
+                               multiple of 64 in [64, 4096] (bf16/int8) or 256/512 (fp32).      */
     uint32_t flags;         /* PA_FLAG_*                                                        */
 } pa_config;
 
@@ -185,9 +188,11 @@ pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg,
                        void* k_cache, void* v_cache,
                        float* k_scale, float* v_scale, float* k_absmax, float* v_absmax);
 
-/* Bytes of device workspace pa_paged_decode needs for this shape (0 when no sequence needs more
- * than one partition). The workspace holds per-partition partial results of one call; its
- * contents need no initialisation, and calls that share a workspace must not run concurrently. */
+/* Bytes of device workspace pa_paged_decode / pa_paged_decode_append need for up to num_seqs
+ * sequences of up to max_context_len tokens. bf16/int8 caches always need one (split partial
+ * results and per-sequence offsets); fp32 caches only when a sequence spans several partitions
+ * (else 0). The contents need no initialisation, and calls that share a workspace must not run
+ * concurrently. */
 pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs,
                                    int32_t max_context_len, size_t* bytes);
 
@@ -200,9 +205,8 @@ pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs,
  *   max_context_len: host-side upper bound of context_lens (sizes the grid); tokens beyond it,
  *   or beyond max_blocks_per_seq * block_size, are not read. Tokens whose table entry lies
  *   outside [0, num_blocks) read as zero keys and values (never dereferenced).
- * Sequences longer than one partition (cfg->partition_size) are split across workgroups and
- * merged with a log-sum-exp reduction through `workspace`. A sequence with context_len <= 0
- * produces zeros. */
+ * Long sequences are split across workgroups (cfg->partition_size) and merged with a log-sum-exp
+ * reduction through `workspace`. A sequence with context_len <= 0 produces zeros. */
 pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
                           const void* k_cache, const void* v_cache,
                           const float* k_scale, const float* v_scale,
@@ -232,7 +236,8 @@ pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float*
  * so keys are positions [0, prefix_lens[s] + chunk_len[s]) read through block_tables[s].
  * Query i attends to keys 0 .. prefix_lens[s] + i (bottom-right aligned causal mask,
  * StandardPagedAttentionKernel.cs:219-255); see PA_FLAG_REFERENCE_LITERAL_MASK.
- *   out: [total_q][num_q_heads][head_dim] fp32, q: [total_q][num_q_heads][head_dim] BF16.
+ *   out: [total_q][num_q_heads][head_dim] fp32, q: [total_q][num_q_heads][head_dim] of
+ *   cfg->q_dtype (BF16 or FP32); the cache must be BF16 or INT8.
  *   max_chunk_len: host-side upper bound of the chunk lengths. */
 pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
                              const int32_t* q_start_loc, const int32_t* prefix_lens,

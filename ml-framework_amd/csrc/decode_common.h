@@ -21,9 +21,12 @@ struct DecodeArgs {
     const float* v_scale;
     const int32_t* block_tables;
     const int32_t* context_lens;
-    float* ws_o;  // [num_seqs][Hq][max_parts][D]
-    float* ws_m;  // [num_seqs][Hq][max_parts]
-    float* ws_l;  // [num_seqs][Hq][max_parts]
+    // split-K partials. fp32 kernel: row = (seq * Hq + head) * max_parts + part. MFMA kernel:
+    // row = slot * G + head-in-group, slot = 2 * range + (0: first segment of the range, 1: last).
+    float* ws_o;  // [rows][D], unnormalised
+    float* ws_m;  // [rows]
+    float* ws_l;  // [rows]
+    int32_t* ws_pref;  // MFMA kernel: [num_seqs + 1] blocks per KV-head row before each sequence
     // fused append (pa_paged_decode_append): the token at position context_len - 1
     const void* k_new;  // [num_seqs][Hkv][D] of the activation dtype
     const void* v_new;
@@ -35,16 +38,18 @@ struct DecodeArgs {
     int32_t num_blocks;
     int32_t max_context_len;
     int32_t max_parts;
-    int32_t part;  // partition length in tokens (multiple of 64)
+    int32_t part;  // fp32 kernel: partition length in tokens
+    // MFMA kernel: the flattened (sequence, KV head, block) list is cut into ranges of
+    // split_blocks blocks (0: ceil(total / split_grid) rounded up to a multiple of 4, at least 4)
+    int32_t split_blocks;
+    int32_t split_grid;
     int32_t q_bf16;
     float scale;
 };
 
-__device__ __forceinline__ int clamp_len(const DecodeArgs& a, int seq) {
-    int T = a.context_lens[seq];
-    T = min(T, a.max_blocks_per_seq * pa::kBlockSize);
-    T = min(T, a.max_context_len);
-    return T;
+// Context length clamped to what the table holds and to max_context_len (raw: context_lens[seq]).
+__device__ __forceinline__ int clamp_len(const DecodeArgs& a, int raw) {
+    return min(min(raw, a.max_blocks_per_seq * pa::kBlockSize), a.max_context_len);
 }
 
 // Final write of one (sequence, query head, dim): normalised output, or the partition's partial.
@@ -107,11 +112,12 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, KV head): wave w takes query heads
-// w, w + 4, ... Partition statistics are read 64 at a time (one per lane); the weighted sum over
-// partitions issues its loads in groups of 8 so their latencies overlap.
-template <int D>
-__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts) {
+// Log-sum-exp merge of the partials of one (sequence, KV head): wave w takes query heads
+// w, w + 4, ...; lane l owns dims l, l + 64, ... The loads of 16 partials (max, sum, outputs) are
+// issued together so their latencies overlap. pidx_of(u, g) is the workspace row of partial u of
+// head g of the group.
+template <int D, typename PidxOf>
+__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
     constexpr int DPL = D / 64;  // dims per lane
     constexpr int CHUNK = 16;    // partitions whose loads are issued together
     const int lane = threadIdx.x & 63;
@@ -119,7 +125,6 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
     const int G = a.group;
     for (int g = wave; g < G; g += 4) {
         const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
-        const int64_t base = row * a.max_parts;
         float M = -INFINITY, L = 0.0f;
         float o[DPL];
 #pragma unroll
@@ -132,7 +137,7 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
 #pragma unroll
             for (int u = 0; u < CHUNK; u++) {
                 const bool ok = u < cnt;
-                const int64_t pi = base + p0 + (ok ? u : 0);
+                const int64_t pi = pidx_of(p0 + (ok ? u : 0), g);
                 pm[u] = ok ? a.ws_m[pi] : -INFINITY;
                 pl[u] = ok ? a.ws_l[pi] : 0.0f;
 #pragma unroll
@@ -164,11 +169,49 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
     const int kvh = blockIdx.x, seq = blockIdx.y;
-    const int T = clamp_len(a, seq);
+    const int T = clamp_len(a, a.context_lens[seq]);
     if (T <= 0) return;
     const int nparts = (T + a.part - 1) / a.part;
     if (nparts <= 1) return;
-    merge_partitions<D>(a, seq, kvh, nparts);
+    merge_partitions<D>(a, seq, kvh, nparts, [&](int u, int g) {
+        return (static_cast<int64_t>(seq) * a.num_kv_heads * a.group + kvh * a.group + g) * a.max_parts + u;
+    });
+}
+
+// Range length (blocks) of the MFMA kernel's split of the `total` blocks of all sequences (one KV
+// head's worth); the decode and the merge kernel derive the same value from the same arguments.
+// By default the split_grid workgroups form split_grid / Hkv ranges, each range done by Hkv
+// workgroups, one per KV head; ranges hold 4 to 256 blocks (more ranges than workgroups when
+// 256 is not enough: workgroups then walk several units).
+__device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64_t total) {
+    if (a.split_blocks > 0) return a.split_blocks;
+    const int64_t nr = a.split_grid >= a.num_kv_heads ? a.split_grid / a.num_kv_heads : 1;
+    int64_t c = (total + nr - 1) / nr;
+    c = (c + 3) & ~static_cast<int64_t>(3);
+    return c < 4 ? 4 : (c > 256 ? 256 : c);  // 256: a wave's block ids fit one VGPR
+}
+
+// Merge pass of the MFMA kernel: one workgroup per (KV head, sequence). Sequence seq occupies
+// blocks [R0, R0 + nbr) of the sequence-major block list; its rows were split iff R0 and
+// R0 + nbr - 1 fall in different ranges, and then ranges w1 .. w2 each left one partial per KV
+// head, in unit u = w * Hkv + kvh: slot 2u, except range w1 when the sequence starts inside it (the
+// row is then that unit's last segment, slot 2u + 1).
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const DecodeArgs a, int32_t num_seqs) {
+    const int kvh = blockIdx.x, seq = blockIdx.y;
+    const int64_t R0 = a.ws_pref[seq];
+    const int nbr = a.ws_pref[seq + 1] - a.ws_pref[seq];
+    if (nbr <= 0) return;
+    const int Hkv = a.num_kv_heads;
+    const int64_t C = split_range_blocks(a, a.ws_pref[num_seqs]);
+    const int64_t w1 = R0 / C, w2 = (R0 + nbr - 1) / C;
+    if (w1 == w2) return;  // written whole by the decode kernel
+    const bool starts_inside = R0 != w1 * C;
+    const int G = a.group;
+    merge_partitions<D>(a, seq, kvh, static_cast<int>(w2 - w1 + 1), [&](int u, int g) {
+        const int64_t unit = (w1 + u) * Hkv + kvh;
+        return (2 * unit + (u == 0 && starts_inside ? 1 : 0)) * G + g;
+    });
 }
 
 __device__ __forceinline__ bf16x8_t k_operand(const uint4& r) { return __builtin_bit_cast(bf16x8_t, r); }
@@ -344,14 +387,16 @@ template <> __device__ __forceinline__ uint32_t buffer_load<uint32_t>(__amdgpu_b
 
 // ---- launchers (one translation unit per kernel family) ----------------------------------------
 constexpr int kMaxPersistentSeqs = 2048;  // per-sequence tables of the persistent kernel (LDS)
+constexpr int kMaxDecodeGrid = 2048;      // persistent workgroups of one MFMA decode launch, at most
 int device_cus();
-// bf16 / int8 caches; num_seqs < kMaxPersistentSeqs; max_items bounds the useful grid.
-void launch_decode_mfma_d64(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
-                            int64_t max_items, hipStream_t s);
-void launch_decode_mfma_d128(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
-                             int64_t max_items, hipStream_t s);
-void launch_decode_mfma_d256(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
-                             int64_t max_items, hipStream_t s);
+// bf16 / int8 caches; num_seqs < kMaxPersistentSeqs. Launches min(resident workgroups, max_grid)
+// workgroups and records that count in a.split_grid (the merge kernel needs it).
+void launch_decode_mfma_d64(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
+                            hipStream_t s);
+void launch_decode_mfma_d128(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
+                             hipStream_t s);
+void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
+                             hipStream_t s);
 // fp32 caches: grid (max_parts, Hkv, num_seqs); returns false for an uncompiled shape.
 bool launch_decode_fp32(const DecodeArgs& a, int head_dim, dim3 grid, hipStream_t s);
 

@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void paged_decode_fp32_kernel(const DecodeArgs
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int Hkv = a.num_kv_heads, Hq = Hkv * G;
 
-    const int T = clamp_len(a, seq);
+    const int T = clamp_len(a, a.context_lens[seq]);
     const int tok0 = part * PART;
     if (T <= 0) {
         if (part == 0)

@@ -1,16 +1,26 @@
-// decode_mfma.h -- the bf16 / int8 paged-decode kernel (MFMA, persistent workgroups).
+// decode_mfma.h -- the bf16 / int8 paged-decode kernel (MFMA, persistent workgroups, balanced split).
 //
-// Work item = (sequence, KV head, partition of `a.part` tokens). A persistent workgroup (4 waves)
-// walks the compacted item list with a stride of gridDim.x; each item's 16-token blocks are dealt
-// to the waves round-robin (block lb0 + wave + 4j). While an item streams, the next item's block
-// ids are already in flight, so an item starts with one memory round trip (its first K/V blocks).
+// Work split: the batch's sequences, as runs of 16-token blocks, are laid end to end and cut into
+// ranges of equal block count. A unit is (range, KV head); by default there is one unit per
+// persistent workgroup (with a fixed range length, workgroups walk units with a stride of
+// gridDim.x). A range covers the tail of one sequence, whole sequences and the head of another;
+// each piece, for the unit's KV head, is a segment. A segment that is a whole row (sequence, KV
+// head) writes the normalised output directly; the (at most two) partial segments of a unit write
+// (max, sum, unnormalised O) to workspace slots 2 * unit + {0: first, 1: last}, and
+// paged_decode_merge_split_kernel combines the slots of every split row. Every workgroup thus
+// streams the same number of K/V bytes whatever the mix of context lengths, and the Hkv
+// workgroups of a range read the same physical blocks at about the same time.
+//
+// Per segment (at most 256 blocks), its blocks are dealt to the 4 waves round-robin (block
+// b0 + wave + 4j), so a wave's block ids fit one VGPR (lane j: its j-th block). The next segment's
+// ids are loaded while the current one streams, so a segment starts with one memory round trip.
 //
 // Per block and wave: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads
 // padded to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16
 // with P split into bf16 high and low parts (~16 significant bits). The score layout the first
 // MFMA leaves in registers (lane = (token group q4, head n)) is the A-operand layout of the second,
 // so P never leaves registers. Three rotating register buffers keep two blocks in flight while a
-// third is consumed. The four waves' (max, sum, O) are combined through LDS at the item's end.
+// third is consumed. The four waves' (max, sum, O) are combined through LDS at the segment's end.
 #pragma once
 
 #include "decode_common.h"
@@ -25,34 +35,33 @@ constexpr float kRescaleThreshold = 8.0f;
 struct MfmaShared {
     float m[4][16];
     float l[4][16];
-    int pref[kMaxPersistentSeqs + 1];  // items (partitions) before sequence s
+    int pref[kMaxPersistentSeqs + 1];  // blocks (per KV head row) before sequence s
     int lens[kMaxPersistentSeqs];      // clamped context length of sequence s
 };
 
-struct ItemMeta {
-    int seq, kvh, part, T;
+// Blocks [b0, b1) of row (seq, kvh); slot < 0: the whole row (final output), else workspace slot.
+struct Segment {
+    int seq, kvh, b0, b1, T, slot;
 };
 
-// Ids of this wave's blocks of an item: lane j holds block lb0 + wave + 4j (or -1: beyond the
-// item, or outside [0, num_blocks)).
-__device__ __forceinline__ int load_block_ids(const DecodeArgs& a, const ItemMeta& m, int wave, int lane) {
-    if (m.T <= 0) return -1;
-    const int tok0 = m.part * a.part;
-    const int tok_end = min(m.T, tok0 + a.part);
-    const int nblk = (tok_end - tok0 + 15) / 16;
-    const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;
+constexpr int kMaxSegmentBlocks = 256;  // 64 per wave: one block id per lane
+
+// Ids of this wave's blocks of a segment: lane j holds block b0 + wave + 4j (-1 beyond the
+// segment). Ids are range-checked where they are used (valid_bid): a check here would make the
+// wave wait for the table load at the point of issue instead of when the id is needed.
+__device__ __forceinline__ int segment_ids(const DecodeArgs& a, const Segment& g, int wave, int lane) {
+    const int b = g.b0 + wave + 4 * lane;
     int id = -1;
-    if (lane < nb) {
-        id = a.block_tables[static_cast<int64_t>(m.seq) * a.max_blocks_per_seq + tok0 / 16 + wave + 4 * lane];
-        if (id >= a.num_blocks) id = -1;
-    }
+    if (b < g.b1) id = a.block_tables[static_cast<int64_t>(g.seq) * a.max_blocks_per_seq + b];
     return id;
 }
+__device__ __forceinline__ int valid_bid(const DecodeArgs& a, int id) { return id < a.num_blocks ? id : -1; }
 
-// One work item. Called by all 256 threads of a workgroup; my_bid from load_block_ids.
-template <int D, int KV, bool QF32, bool APPEND>
-__device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& im, int my_bid, MfmaShared& sh,
-                                          float (*s_x)[D][16]) {
+// One segment. Called by all 256 threads of a workgroup; my_bid = segment_ids(..). prefetch_next()
+// is called once, after the segment's first loads, to start the next segment's id loads.
+template <int D, int KV, bool QF32, bool APPEND, typename Prefetch>
+__device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment& g, int my_bid, MfmaShared& sh,
+                                             float (*s_x)[D][16], Prefetch&& prefetch_next) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
@@ -65,57 +74,41 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
     const int q4 = lane >> 4;  // token group (QK C rows) / k group of the MFMA operands
     const int n = lane & 15;   // head column of S^T / row of P / dim within a PV tile
     const int G = a.group, Hkv = a.num_kv_heads;
-    const int seq = im.seq, kvh = im.kvh, part = im.part, T = im.T;
+    const int seq = g.seq, kvh = g.kvh, T = g.T;
+    const int nblk = g.b1 - g.b0;
+    const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;  // this wave's blocks
+    const int nbrow = (T + 15) / 16;
 
-    if (T <= 0) {
-        for (int idx = tid; idx < G * D; idx += 256)
-            a.out[(static_cast<int64_t>(seq) * Hkv * G + kvh * G) * D + idx] = 0.0f;
-        return;
-    }
-    const int tok0 = part * a.part;
-    const int tok_end = min(T, tok0 + a.part);
-    const int nparts = (T + a.part - 1) / a.part;
-    const int lb0 = tok0 / 16;
-    const int nblk = (tok_end - tok0 + 15) / 16;
-    const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;
-
-    float my_ks = 0.0f, my_vs = 0.0f;
-    if constexpr (KV == PA_DTYPE_INT8) {
-        if (my_bid >= 0) {
-            my_ks = a.k_scale[static_cast<int64_t>(my_bid) * Hkv + kvh];
-            my_vs = a.v_scale[static_cast<int64_t>(my_bid) * Hkv + kvh];
-        }
-    }
-
-    // Fused append: the sequence's last block belongs to wave (rel & 3) at iteration rel >> 2.
-    // That wave fetches the new token now (lane l: dims l*NPL ..) and, for int8, the block's
-    // running statistics, so the patch costs no extra round trip later.
+    // Loads issued at the segment's start, in this order: its first two K/V blocks, the next
+    // segment's block ids (prefetch callback), then Q, the int8 block scales and the appended token.
+    // Memory returns in order, so the K/V requests go out first; none of the other values is
+    // used right after its load (that would stall the wave on the load's latency).
+    float my_ks = 0.0f, my_vs = 0.0f;  // int8: scales of this lane's block
+    // Fused append: the row's last block belongs to wave (rel & 3) at iteration rel >> 2 of the
+    // segment that ends the row. That wave fetches the new token (lane l: dims l*NPL ..) and, for
+    // int8, the block's running statistics; the token's raw bits (fp32, or bf16 packed two per
+    // word) are decoded only at the patch.
+    constexpr int NW = QF32 ? NPL : (NPL + 1) / 2;
     int j_app = -1;
-    float new_k[NPL], new_v[NPL];
+    uint32_t nk_raw[NW], nv_raw[NW];
     Int8Stats old{};
     if constexpr (APPEND) {
-        const int rel = (T - 1) / 16 - lb0;
-        if (part == nparts - 1 && (rel & 3) == wave) j_app = rel >> 2;
-        if (j_app >= 0) {
-            const int64_t src = (static_cast<int64_t>(seq) * Hkv + kvh) * D + lane * NPL;
-#pragma unroll
-            for (int e = 0; e < NPL; e++) {
-                new_k[e] = act_at(a.k_new, QF32, src + e);
-                new_v[e] = act_at(a.v_new, QF32, src + e);
-            }
-            if constexpr (KV == PA_DTYPE_INT8) {
-                const int bid = __builtin_amdgcn_readlane(my_bid, j_app);
-                if (bid >= 0) {
-                    const int64_t sidx = static_cast<int64_t>(bid) * Hkv + kvh;
-                    old = Int8Stats{a.k_absmax[sidx], a.k_scale[sidx], a.v_absmax[sidx], a.v_scale[sidx]};
-                }
-            }
-        }
+        const int rel = nbrow - 1 - g.b0;
+        if (g.b1 == nbrow && (rel & 3) == wave) j_app = rel >> 2;  // always this wave's last block
     }
-
+    // The appending wave consumes its blocks starting with that last one (iteration 0 takes list
+    // entry j_app, iteration j takes entry j - 1): the patch then happens while the pipeline fills
+    // instead of at the end of the segment, where every other wave would wait for it.
+    const bool rot = APPEND && j_app > 0;
+    auto entry = [&](int j) { return rot ? (j == 0 ? j_app : j - 1) : j; };
+    auto new_val = [&](const uint32_t (&raw)[NW], int e) -> float {
+        if constexpr (QF32) return __uint_as_float(raw[e]);
+        else if constexpr (NPL == 1) return __uint_as_float(raw[0] << 16);
+        else return __uint_as_float((e & 1) ? (raw[e >> 1] & 0xffff0000u) : (raw[e >> 1] << 16));
+    };
     // Q^T operand: lane (q4, n) holds head n, dims 32s + 8q4 .. +8 (zero rows for n >= G).
     bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
-    {
+    auto side_loads = [&]() {
         const bool hv = n < G;
         const int64_t qrow = (static_cast<int64_t>(seq) * Hkv * G + kvh * G + (hv ? n : 0)) * D;
 #pragma unroll
@@ -142,7 +135,35 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
                 qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
             }
         }
-    }
+        if constexpr (KV == PA_DTYPE_INT8) {  // unconditional: an invalid block's scales are never used
+            const int sb = my_bid >= 0 && my_bid < a.num_blocks ? my_bid : 0;
+            my_ks = a.k_scale[static_cast<int64_t>(sb) * Hkv + kvh];
+            my_vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + kvh];
+        }
+        if constexpr (APPEND) {
+            if (j_app >= 0) {
+                const int64_t src = (static_cast<int64_t>(seq) * Hkv + kvh) * D + lane * NPL;
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    if constexpr (QF32) {
+                        nk_raw[w] = static_cast<const uint32_t*>(a.k_new)[src + w];
+                        nv_raw[w] = static_cast<const uint32_t*>(a.v_new)[src + w];
+                    } else if constexpr (NPL == 1) {
+                        nk_raw[w] = static_cast<const uint16_t*>(a.k_new)[src];
+                        nv_raw[w] = static_cast<const uint16_t*>(a.v_new)[src];
+                    } else {
+                        nk_raw[w] = static_cast<const uint32_t*>(a.k_new)[(src >> 1) + w];
+                        nv_raw[w] = static_cast<const uint32_t*>(a.v_new)[(src >> 1) + w];
+                    }
+                }
+                if constexpr (KV == PA_DTYPE_INT8) {
+                    const int bid = __builtin_amdgcn_readlane(my_bid, j_app);  // list entry j_app
+                    const int64_t sidx = static_cast<int64_t>(bid >= 0 && bid < a.num_blocks ? bid : 0) * Hkv + kvh;
+                    old = Int8Stats{a.k_absmax[sidx], a.k_scale[sidx], a.v_absmax[sidx], a.v_scale[sidx]};
+                }
+            }
+        }
+    };
 
     const char* kc = static_cast<const char*>(a.k_cache);
     const char* vc = static_cast<const char*>(a.v_cache);
@@ -155,7 +176,7 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
     // The load sequence is therefore identical on every iteration (no branches), which lets the
     // compiler wait for exactly the oldest block instead of draining every load in flight.
     auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
-        const int bid = j < nb ? __builtin_amdgcn_readlane(my_bid, j & 63) : -1;
+        const int bid = j < nb ? valid_bid(a, __builtin_amdgcn_readlane(my_bid, entry(j) & 63)) : -1;
         const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
         const int bytes = bid >= 0 ? TILE * ELT : 0;
         const __amdgpu_buffer_rsrc_t rk =
@@ -175,29 +196,39 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
     for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
+        const int e = entry(j);
+        const int bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, e));
         float ks = 1.0f, vfac = 1.0f;
         if constexpr (KV == PA_DTYPE_INT8) {
-            ks = readlane_f(my_ks, j);
-            vfac = readlane_f(my_vs, j);
+            ks = bid >= 0 ? readlane_f(my_ks, e) : 0.0f;
+            vfac = bid >= 0 ? readlane_f(my_vs, e) : 0.0f;
         }
         if constexpr (APPEND) {
-            const int bid = __builtin_amdgcn_readlane(my_bid, j);
-            if (j == j_app && bid >= 0) {
-                // Stage the new token in LDS (free during streaming: the previous item's combine
-                // ended with a barrier, this item's starts with one), then patch the tile.
+            if (e == j_app && bid >= 0) {
+                // Stage the new token in LDS (free during streaming: the previous segment's
+                // combine ended with a barrier, this one's starts with one), then patch the tile.
                 float* s_new = &s_x[0][0][0];
+                // The empty asm keeps the decoding here: hoisted out of the loop, it would wait
+                // for the token's loads before the first block.
+                uint32_t kw[NW], vw[NW];
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    kw[w] = nk_raw[w];
+                    vw[w] = nv_raw[w];
+                    asm volatile("" : "+v"(kw[w]), "+v"(vw[w]));
+                }
 #pragma unroll
                 for (int e = 0; e < NPL; e++) {
-                    s_new[lane * NPL + e] = new_k[e];
-                    s_new[D + lane * NPL + e] = new_v[e];
+                    s_new[lane * NPL + e] = new_val(kw, e);
+                    s_new[D + lane * NPL + e] = new_val(vw, e);
                 }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the stores have landed in LDS
                 __builtin_amdgcn_wave_barrier();
                 const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * TILE;
                 const int r = (T - 1) & 15;
                 if constexpr (KV == PA_DTYPE_INT8)
-                    append_int8_regs<D>(a, tile, static_cast<int64_t>(bid) * Hkv + kvh, s_new, r, q4, n, old, kr, vr,
-                                        ks, vfac);
+                    append_int8_regs<D>(a, tile, static_cast<int64_t>(bid) * Hkv + kvh, s_new, r, q4, n, old, kr,
+                                        vr, ks, vfac);
                 else
                     append_bf16_regs<D>(a, tile, s_new, r, q4, n, kr, vr);
             }
@@ -210,7 +241,7 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
             s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
             if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
         }
-        const int tbase = (lb0 + wave + 4 * j) * 16 + 4 * q4;
+        const int tbase = (g.b0 + wave + 4 * e) * 16 + 4 * q4;
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -268,6 +299,8 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
         int j = 0;
         load(ka, va, 0);
         load(kb, vb, 1);
+        prefetch_next();
+        side_loads();
         while (j < nb) {
             load(kx, vx, j + 2);
             compute(ka, va, j);
@@ -334,13 +367,12 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
             for (int i = 0; i < 4; i++) {
                 const int h = 4 * q4 + i;
                 if (h >= G) break;
-                const int64_t row = row0 + h;
-                if (nparts == 1) {
+                if (g.slot < 0) {
                     const float inv = 1.0f / L[i];
 #pragma unroll
-                    for (int t = 0; t < NT; t++) a.out[row * D + 16 * t + n] = acc[t][i] * inv;
+                    for (int t = 0; t < NT; t++) a.out[(row0 + h) * D + 16 * t + n] = acc[t][i] * inv;
                 } else {
-                    const int64_t pidx = row * a.max_parts + part;
+                    const int64_t pidx = static_cast<int64_t>(g.slot) * G + h;
 #pragma unroll
                     for (int t = 0; t < NT; t++) a.ws_o[pidx * D + 16 * t + n] = acc[t][i];
                     if (n == 0) {
@@ -351,22 +383,25 @@ __device__ __forceinline__ void mfma_item(const DecodeArgs& a, const ItemMeta& i
             }
         }
     }
-    __syncthreads();  // LDS reuse by the next item
+    __syncthreads();  // LDS reuse by the next segment
 }
 
-// Persistent mode: gridDim.x workgroups walk the compacted list of non-empty items
-// (sequence s owns items pref[s]*Hkv .. pref[s+1]*Hkv - 1, KV head fastest), item w, w + grid, ...
-// Every workgroup leaves its loop after a bounded number of items.
+// Persistent decode kernel over at most kMaxPersistentSeqs - 1 sequences.
 template <int D, int KV, bool QF32, bool APPEND>
-__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a, int32_t num_seqs) {
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a,
+                                                                                          int32_t num_seqs) {
     __shared__ MfmaShared sh;
     __shared__ float s_x[2][D][16];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // Items per sequence: its partition count (a zero-length sequence still gets one item, which
-    // writes its zero output). Exclusive prefix over sequences, built by the whole workgroup.
+    // Blocks per row of each sequence; exclusive prefix over sequences, built by the workgroup.
+    // All PER lengths are loaded before any is used, so the loads overlap (a use between them would
+    // serialise PER memory round trips).
     constexpr int PER = (kMaxPersistentSeqs + 255) / 256;
+    int raw[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) raw[k] = a.context_lens[min(tid * PER + k, num_seqs - 1)];
     int cnt[PER];
     int local = 0;
 #pragma unroll
@@ -374,9 +409,9 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persis
         const int s = tid * PER + k;
         int c = 0;
         if (s < num_seqs) {
-            const int T = clamp_len(a, s);
+            const int T = clamp_len(a, raw[k]);
             sh.lens[s] = T;
-            c = T <= 0 ? 1 : (T + a.part - 1) / a.part;
+            c = T <= 0 ? 0 : (T + 15) / 16;
         }
         cnt[k] = c;
         local += c;
@@ -391,44 +426,73 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persis
     __syncthreads();
     int wave_off = 0;
     for (int w = 0; w < wave; w++) wave_off += sh.pref[w];
-    const int total_parts = sh.pref[0] + sh.pref[1] + sh.pref[2] + sh.pref[3];
     __syncthreads();
     int run = wave_off + incl - local;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int s = tid * PER + k;
-        if (s <= num_seqs) sh.pref[s] = run;
+        if (s <= num_seqs) {
+            sh.pref[s] = run;
+            if (blockIdx.x == 0) a.ws_pref[s] = run;  // read by the merge kernel
+        }
         run += cnt[k];
     }
     __syncthreads();
 
     const int Hkv = a.num_kv_heads;
-    const int64_t total = static_cast<int64_t>(total_parts) * Hkv;
-    int seq = 0;  // items only increase, so the owning sequence is found by scanning forward
-    auto meta_of = [&](int64_t item) -> ItemMeta {
-        const int pi = static_cast<int>(item / Hkv);
-        const int kvh = static_cast<int>(item - static_cast<int64_t>(pi) * Hkv);
-        while (seq + 1 < num_seqs && sh.pref[seq + 1] <= pi) seq++;
-        return ItemMeta{seq, kvh, pi - sh.pref[seq], sh.lens[seq]};
-    };
-    int64_t item = blockIdx.x;
-    if (item >= total) return;
-    ItemMeta cur = meta_of(item);
-    int cur_bid = load_block_ids(a, cur, wave, lane);
-    for (;;) {
-        const int64_t next = item + gridDim.x;
-        const bool has_next = next < total;
-        ItemMeta nxt{0, 0, 0, 0};
-        int nxt_bid = -1;
-        if (has_next) {  // issued before this item's K/V loads, consumed by the next iteration
-            nxt = meta_of(next);
-            nxt_bid = load_block_ids(a, nxt, wave, lane);
+    // Sequences with no context produce zeros.
+    for (int s = blockIdx.x; s < num_seqs; s += gridDim.x) {
+        if (sh.lens[s] > 0) continue;
+        const int n = Hkv * a.group * D;
+        for (int idx = tid; idx < n; idx += 256) a.out[static_cast<int64_t>(s) * n + idx] = 0.0f;
+    }
+
+    // Units u = range * Hkv + kvh; unit u walks blocks [range * C, (range + 1) * C) of the
+    // sequence-major block list for KV head kvh. Workgroups u .. u + Hkv - 1 run together and read
+    // the same physical blocks (all KV heads of a block are one contiguous Hkv * 16 * D run).
+    const int64_t total = sh.pref[num_seqs];
+    if (total == 0) return;
+    const int64_t C = split_range_blocks(a, total);
+    const int64_t units = (total + C - 1) / C * Hkv;
+    int64_t u = blockIdx.x;
+    if (u >= units) return;
+    int64_t r = u / Hkv;
+    int kvh = static_cast<int>(u - r * Hkv);
+    int64_t p = r * C, end = min(total, p + C);
+    int seq = 0;  // scanned forward while positions increase
+    auto next_segment = [&](Segment& g) -> bool {
+        if (p >= end) {
+            u += gridDim.x;
+            if (u >= units) return false;
+            r = u / Hkv;
+            kvh = static_cast<int>(u - r * Hkv);
+            p = r * C;
+            end = min(total, p + C);
+            if (sh.pref[seq] > p) seq = 0;
         }
-        mfma_item<D, KV, QF32, APPEND>(a, cur, cur_bid, sh, s_x);
+        while (sh.pref[seq + 1] <= p) seq++;
+        const int nbr = sh.pref[seq + 1] - sh.pref[seq];
+        const int b0 = static_cast<int>(p - sh.pref[seq]);
+        const int b1 = static_cast<int>(min(static_cast<int64_t>(nbr), b0 + (end - p)));
+        const int slot = (b0 == 0 && b1 == nbr) ? -1 : static_cast<int>(2 * u + (p == r * C ? 0 : 1));
+        g = Segment{seq, kvh, b0, b1, sh.lens[seq], slot};
+        p += b1 - b0;
+        return true;
+    };
+    Segment cur;
+    next_segment(cur);
+    int cur_ids = segment_ids(a, cur, wave, lane);
+    for (;;) {
+        Segment nxt;
+        bool has_next = false;
+        int nxt_ids = -1;
+        mfma_segment<D, KV, QF32, APPEND>(a, cur, cur_ids, sh, s_x, [&]() {
+            has_next = next_segment(nxt);
+            if (has_next) nxt_ids = segment_ids(a, nxt, wave, lane);  // in flight during this segment
+        });
         if (!has_next) break;
-        item = next;
         cur = nxt;
-        cur_bid = nxt_bid;
+        cur_ids = nxt_ids;
     }
 }
 

@@ -5,7 +5,7 @@ namespace pa {
 namespace {
 
 template <int D, int KV, bool QF32, bool APPEND>
-void launch_one(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_t s) {
+void launch_one(DecodeArgs& a, int num_seqs, int64_t max_grid, hipStream_t s) {
     auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND>;
     // Resident workgroups per CU for this instance (queried once; read-only afterwards).
     static const int per_cu = [&] {
@@ -14,27 +14,30 @@ void launch_one(const DecodeArgs& a, int num_seqs, int64_t max_items, hipStream_
         return n;
     }();
     int64_t nwg = static_cast<int64_t>(device_cus()) * per_cu;
-    if (nwg > max_items) nwg = max_items;
+    if (nwg > kMaxDecodeGrid) nwg = kMaxDecodeGrid;
+    if (nwg >= a.num_kv_heads) nwg -= nwg % a.num_kv_heads;  // whole ranges (one unit per KV head)
+    if (nwg > max_grid) nwg = max_grid;
     if (nwg < 1) nwg = 1;
+    a.split_grid = static_cast<int32_t>(nwg);
     kern<<<static_cast<unsigned>(nwg), 256, 0, s>>>(a, num_seqs);
 }
 
 template <int KV, bool QF32>
-void pick_append(const DecodeArgs& a, bool append, int num_seqs, int64_t max_items, hipStream_t s) {
-    if (append) launch_one<256, KV, QF32, true>(a, num_seqs, max_items, s);
-    else launch_one<256, KV, QF32, false>(a, num_seqs, max_items, s);
+void pick_append(DecodeArgs& a, bool append, int num_seqs, int64_t max_grid, hipStream_t s) {
+    if (append) launch_one<256, KV, QF32, true>(a, num_seqs, max_grid, s);
+    else launch_one<256, KV, QF32, false>(a, num_seqs, max_grid, s);
 }
 
 }  // namespace
 
-void launch_decode_mfma_d256(const DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
-                            int64_t max_items, hipStream_t s) {
+void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+                            int64_t max_grid, hipStream_t s) {
     if (kv_dtype == PA_DTYPE_BF16) {
-        if (q_f32) pick_append<PA_DTYPE_BF16, true>(a, append, num_seqs, max_items, s);
-        else pick_append<PA_DTYPE_BF16, false>(a, append, num_seqs, max_items, s);
+        if (q_f32) pick_append<PA_DTYPE_BF16, true>(a, append, num_seqs, max_grid, s);
+        else pick_append<PA_DTYPE_BF16, false>(a, append, num_seqs, max_grid, s);
     } else {
-        if (q_f32) pick_append<PA_DTYPE_INT8, true>(a, append, num_seqs, max_items, s);
-        else pick_append<PA_DTYPE_INT8, false>(a, append, num_seqs, max_items, s);
+        if (q_f32) pick_append<PA_DTYPE_INT8, true>(a, append, num_seqs, max_grid, s);
+        else pick_append<PA_DTYPE_INT8, false>(a, append, num_seqs, max_grid, s);
     }
 }
 

@@ -2,9 +2,10 @@
 //
 // Fills the no-op placeholders of the reference's append path: PagedAttentionLayer.UpdateKVCache /
 // CopyTensorToBlock (src/MLFramework/Inference/PagedAttention/Layers/PagedAttentionLayer.cs:244-327).
-// Cache layout per layer: [num_blocks][num_kv_heads][16][head_dim] (PagedAttentionLayer.cs:315 for
-// one layer). Both kernels are HBM-bound scatters; the int8 one also owns the per-(block, KV head)
-// scale and running absmax.
+// Cache layout per layer (the reference's [num_blocks][num_kv_heads][block][head_dim] block tensor,
+// PagedAttentionLayer.cs:315, with V transposed per tile): K tile [16 tokens][head_dim], V tile
+// [head_dim][16 tokens], one tile per (block, KV head). Both kernels are HBM-bound scatters; the
+// int8 one also owns the per-(block, KV head) scale and running absmax.
 #include <string>
 
 #include "pa_internal.h"

@@ -5,21 +5,15 @@
 // which gathers each sequence's K/V and calls StandardPagedAttentionKernel once per sequence,
 // Kernels/StandardPagedAttentionKernel.cs:21-84) with one launch over the whole ragged batch.
 //
-// Work decomposition: one workgroup (4 waves) per (partition, KV head, sequence). A partition is a
-// run of `part` tokens (whole 16-token blocks) of one sequence. A sequence that fits in one
-// partition is finished in place; longer ones write per-partition (max, sum, unnormalised output)
-// to the workspace and paged_decode_merge_kernel combines them with a log-sum-exp reduction.
-// The G = Hq / Hkv query heads of a KV head share every K/V byte loaded (GQA).
-//
-// bf16 / int8 caches (paged_decode_mfma_kernel): each wave streams its blocks (every 4th block of
-// the partition) with a one-block prefetch. Per block, S^T[16 tokens][16 heads] = K . Q^T runs on
-// v_mfma_f32_16x16x32_bf16 (query heads padded to 16 rows) and O[16 heads][D] += P . V on
-// v_mfma_f32_16x16x16_bf16 with P split into bf16 high and low parts, so the probabilities keep
-// ~16 bits. The score layout the first MFMA leaves in registers (lane = (token group, head)) is
-// exactly the A-operand layout of the second, so P never leaves registers. Softmax is online per
-// wave in fp32; the four waves are combined through LDS at the end.
-// fp32 caches (paged_decode_fp32_kernel): VALU dot products reduced across lanes with DPP, a
-// partition-wide softmax in LDS, and VALU P.V.
+// bf16 / int8 caches (decode_mfma.h, paged_decode_mfma_persistent_kernel): persistent workgroups
+// cut the batch's blocks into equal ranges, one (range, KV head) unit each, so every workgroup
+// streams the same bytes whatever the mix of context lengths; rows (sequence, KV head) split
+// between ranges leave (max, sum, unnormalised O) partials that paged_decode_merge_split_kernel
+// combines with a log-sum-exp reduction. The G = Hq / Hkv query heads of a KV head share every
+// K/V byte loaded (GQA): QK and PV run on MFMA with the heads as the 16 MFMA rows.
+// fp32 caches (decode_fp32.h): one workgroup per (partition, KV head, sequence), VALU dot products
+// reduced across lanes with DPP, a partition-wide softmax in LDS, VALU P.V, and the same kind of
+// merge over fixed 256/512-token partitions (paged_decode_merge_kernel).
 #include <string>
 
 #include "decode_common.h"
@@ -47,14 +41,10 @@ using pa::DecodeArgs;
 using pa::clamp_len;
 using pa::act_at;
 
-constexpr int kMaxPart = 4096;  // a wave's block ids must fit one VGPR (64 lanes x 4 waves x 16)
-
-// Partition length for this call. fp32 caches use 256 or 512 (VALU kernel templates); bf16/int8
-// take any multiple of 64 up to 4096. The default is about a fifth of the longest context, rounded
-// up to 256 and clamped to [256, 2048]: long enough that a partition's fixed costs (its first
-// block loads, the four-wave combine, the partial write) stay small next to its streaming time,
-// short enough that long sequences split into several work items for load balance.
-int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
+// Split length for this call. fp32 caches use partitions of 256 or 512 tokens (VALU kernel
+// templates). bf16/int8 caches: 0 lets the kernel cut the batch's blocks into one equal range per
+// resident workgroup; otherwise the ranges are `partition_size` tokens (multiple of 64).
+int resolve_part(const pa_config* cfg, std::string* err) {
     const int req = cfg->partition_size;
     if (cfg->kv_dtype == PA_DTYPE_FP32) {
         if (req == 0) return 256;
@@ -62,23 +52,41 @@ int resolve_part(const pa_config* cfg, int32_t max_len, std::string* err) {
         *err = "partition_size must be 0, 256 or 512 for an fp32 cache";
         return -1;
     }
-    if (req == 0) {
-        int p = (max_len + 4) / 5;
-        p = (p + 255) / 256 * 256;
-        return p < 256 ? 256 : (p > 2048 ? 2048 : p);
-    }
-    if (req < 64 || req > kMaxPart || req % 64 != 0) {
-        *err = "partition_size must be a multiple of 64 in [64, 4096]";
+    if (req == 0) return 0;
+    if (req < 64 || req > 4096 || req % 64 != 0) {
+        *err = "partition_size must be 0 or a multiple of 64 in [64, 4096]";
         return -1;
     }
     return req;
 }
 
+// Units (range, KV head) an MFMA launch over (at most) this shape can produce: the bound the
+// workspace is sized for. By default ranges hold 4 to 256 blocks and there are at most
+// max(kMaxDecodeGrid / Hkv, blocks / 256) of them.
+int64_t mfma_max_units(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
+    const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
+    const int64_t wmax = seqs * ((static_cast<int64_t>(max_len) + 15) / 16);
+    const int64_t hkv = cfg->num_kv_heads;
+    if (wmax <= 0) return 0;
+    if (part > 0) return (wmax + part / 16 - 1) / (part / 16) * hkv;
+    int64_t r = pa::kMaxDecodeGrid >= hkv ? pa::kMaxDecodeGrid / hkv : 1;
+    const int64_t by_max_len = (wmax + 255) / 256;
+    if (r < by_max_len) r = by_max_len;
+    const int64_t by_min_len = (wmax + 3) / 4;
+    return (r < by_min_len ? r : by_min_len) * hkv;
+}
+
 size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
-    const int64_t max_parts = (static_cast<int64_t>(max_len) + part - 1) / part;
-    if (max_parts <= 1 || num_seqs <= 0) return 0;
-    const int64_t rows = static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts;
-    return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float);
+    if (num_seqs <= 0) return 0;
+    if (cfg->kv_dtype == PA_DTYPE_FP32) {
+        const int64_t max_parts = (static_cast<int64_t>(max_len) + part - 1) / part;
+        if (max_parts <= 1) return 0;
+        const int64_t rows = static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts;
+        return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float);
+    }
+    const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
+    const int64_t rows = 2 * mfma_max_units(cfg, num_seqs, max_len, part) * (cfg->num_q_heads / cfg->num_kv_heads);
+    return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float) + static_cast<size_t>(seqs + 1) * 4;
 }
 
 int32_t effective_max_len(int32_t max_context_len, int32_t max_blocks_per_seq) {
@@ -87,14 +95,12 @@ int32_t effective_max_len(int32_t max_context_len, int32_t max_blocks_per_seq) {
     return max_context_len > table_tokens ? static_cast<int32_t>(table_tokens) : max_context_len;
 }
 
-// Resident workgroups per CU of a kernel, and CUs of the current device (queried once each;
-// read-only afterwards).
 
 // fp32 caches, fused entry point: append the token at position context_len - 1 of every
 // sequence (one workgroup per sequence, K row and V column of every KV head), before the decode.
 __global__ __launch_bounds__(256) void append_last_token_fp32_kernel(const DecodeArgs a, int32_t head_dim) {
     const int seq = blockIdx.x;
-    const int T = clamp_len(a, seq);
+    const int T = clamp_len(a, a.context_lens[seq]);
     if (T <= 0) return;
     const int bid = a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + (T - 1) / 16];
     if (bid < 0 || bid >= a.num_blocks) return;
@@ -124,7 +130,7 @@ pa_status pa_decode_workspace_size(const pa_config* cfg, int32_t num_seqs, int32
     if (num_seqs < 0 || max_context_len < 0)
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_decode_workspace_size: negative size");
     std::string err;
-    const int part = resolve_part(cfg, max_context_len, &err);
+    const int part = resolve_part(cfg, &err);
     if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_decode_workspace_size: " + err);
     *bytes = workspace_bytes_for(cfg, num_seqs, max_context_len, part);
     return pa::clear_error();
@@ -162,11 +168,11 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
 
     const int32_t max_len = effective_max_len(max_context_len, max_blocks_per_seq);
     std::string err;
-    // The partition length is resolved from the caller's max_context_len, exactly as
-    // pa_decode_workspace_size does, so both agree on the workspace layout.
-    const int part = resolve_part(cfg, max_context_len, &err);
+    const int part = resolve_part(cfg, &err);
     if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": " + err);
-    const int32_t max_parts = max_len > 0 ? (max_len + part - 1) / part : 1;
+    const bool fp32 = cfg->kv_dtype == PA_DTYPE_FP32;
+    const int32_t max_parts = fp32 && max_len > 0 ? (max_len + part - 1) / part : 1;
+    // max_len <= max_context_len, so a workspace sized by pa_decode_workspace_size suffices.
     const size_t need = workspace_bytes_for(cfg, num_seqs, max_len, part);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return pa::set_error(PA_ERROR_WORKSPACE_TOO_SMALL,
@@ -192,13 +198,16 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     a.max_context_len = max_len;
     a.max_parts = max_parts;
     a.part = part;
+    a.split_blocks = fp32 ? 0 : part / 16;
     a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
     a.scale = pa::resolve_scale(cfg);
+    const int64_t max_units = fp32 ? 0 : mfma_max_units(cfg, num_seqs, max_len, part);
     if (need > 0) {
-        const int64_t rows = static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts;
+        const int64_t rows = fp32 ? static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts : 2 * max_units * G;
         a.ws_o = static_cast<float*>(workspace);
         a.ws_m = a.ws_o + rows * cfg->head_dim;
         a.ws_l = a.ws_m + rows;
+        a.ws_pref = reinterpret_cast<int32_t*>(a.ws_l + rows);
     }
 
     hipStream_t s = pa::native(stream);
@@ -207,22 +216,32 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
         dim3 grid(max_parts, cfg->num_kv_heads, num_seqs);
         if (!pa::launch_decode_fp32(a, cfg->head_dim, grid, s))
             return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": configuration not compiled");
-    } else {
-        const int64_t max_items = static_cast<int64_t>(max_parts) * cfg->num_kv_heads * num_seqs;
-        const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
-        switch (cfg->head_dim) {
-            case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, num_seqs, max_items, s); break;
-            case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, num_seqs, max_items, s); break;
-            default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, append, num_seqs, max_items, s); break;
+        PA_HIP_CHECK(hipGetLastError());
+        if (max_parts > 1) {
+            dim3 mgrid(cfg->num_kv_heads, num_seqs);
+            switch (cfg->head_dim) {
+                case 64: pa::paged_decode_merge_kernel<64><<<mgrid, 256, 0, s>>>(a); break;
+                case 128: pa::paged_decode_merge_kernel<128><<<mgrid, 256, 0, s>>>(a); break;
+                default: pa::paged_decode_merge_kernel<256><<<mgrid, 256, 0, s>>>(a); break;
+            }
+            PA_HIP_CHECK(hipGetLastError());
         }
+        return pa::clear_error();
+    }
+    const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
+    const int64_t max_grid = max_units > 0 ? max_units : 1;
+    switch (cfg->head_dim) {
+        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
+        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
+        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
-    if (max_parts > 1) {
+    if (max_units > cfg->num_kv_heads) {  // more than one range: a row may span two
         dim3 mgrid(cfg->num_kv_heads, num_seqs);
         switch (cfg->head_dim) {
-            case 64: pa::paged_decode_merge_kernel<64><<<mgrid, 256, 0, s>>>(a); break;
-            case 128: pa::paged_decode_merge_kernel<128><<<mgrid, 256, 0, s>>>(a); break;
-            default: pa::paged_decode_merge_kernel<256><<<mgrid, 256, 0, s>>>(a); break;
+            case 64: pa::paged_decode_merge_split_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+            case 128: pa::paged_decode_merge_split_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+            default: pa::paged_decode_merge_split_kernel<256><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
         }
         PA_HIP_CHECK(hipGetLastError());
     }

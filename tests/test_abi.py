@@ -106,17 +106,22 @@ def test_argument_validation():
 
 
 def test_workspace_size():
-    c = cfg()
-    # one partition per sequence: no workspace
-    assert pa.decode_workspace_size(c, 64, 256) == 0
-    # default partition: a fifth of the longest context rounded up to 256, within [256, 2048]:
-    # 4096 -> 1024 -> 4 partitions of (D + 2) floats per query head
-    assert pa.decode_workspace_size(c, 64, 4096) == 64 * 32 * 4 * (128 + 2) * 4
-    # 32768 -> 2048 (clamped) -> 16 partitions
-    assert pa.decode_workspace_size(c, 8, 32768) == 8 * 32 * 16 * 130 * 4
-    assert pa.decode_workspace_size(c, 64, 1000) == 64 * 32 * 4 * 130 * 4  # 1000 -> 256 -> 4 parts
-    assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 64 * 32 * 8 * 130 * 4
+    c = cfg()  # Hq 32, Hkv 8, D 128, bf16
+    # bf16/int8, default split: 2 partial slots per unit (range, KV head) of (D + 2) floats per query
+    # head of the group (G = 4); ranges <= min(2048 / Hkv, ceil(blocks / 4)) where blocks counts one
+    # KV head; plus num_seqs + 1 ints of sequence offsets.
+    # 64 x 4096 tokens = 16384 blocks -> min(256, 4096) = 256 ranges x 8 KV heads
+    assert pa.decode_workspace_size(c, 64, 4096) == 2 * 2048 * 4 * 130 * 4 + 65 * 4
+    # 1 sequence of 16 tokens: 1 block -> 1 range x 8 KV heads
+    assert pa.decode_workspace_size(c, 1, 16) == 2 * 8 * 4 * 130 * 4 + 2 * 4
+    # fixed 512-token ranges (32 blocks): 16384 / 32 = 512 ranges x 8 KV heads
+    assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 2 * 4096 * 4 * 130 * 4 + 65 * 4
+    # beyond one launch's 2047 sequences the launches reuse the workspace: sized for 2047
+    assert pa.decode_workspace_size(c, 5000, 64) == 2 * 2048 * 4 * 130 * 4 + 2048 * 4
+    assert pa.decode_workspace_size(c, 0, 4096) == 0
+    # fp32: per-partition partials only when some sequence needs more than one partition
     assert pa.decode_workspace_size(cfg(kv_dtype=0), 4, 256) == 0
+    assert pa.decode_workspace_size(cfg(kv_dtype=0), 4, 1000) == 4 * 32 * 4 * 130 * 4
     with pytest.raises(pa.PagedAttentionError) as e:
         pa.decode_workspace_size(cfg(partition_size=100), 4, 256)
     assert e.value.status == pa.PA_ERROR_UNSUPPORTED
@@ -128,7 +133,7 @@ def test_last_error_is_per_call():
     with pytest.raises(pa.PagedAttentionError):
         pa.paged_decode(None, cfg(head_dim=48), FAKE, FAKE, FAKE, FAKE, None, None, FAKE, FAKE, 4, 10, 100)
     assert "head_dim" in pa.last_error()
-    assert pa.decode_workspace_size(cfg(), 1, 16) == 0
+    assert pa.decode_workspace_size(cfg(), 1, 16) > 0
     assert pa.last_error() == ""
 
 

@@ -177,7 +177,7 @@ def test_decode_c4_int8_subset(stream):
 EDGE_LENS = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 1023, 1024, 1025, 3000]
 
 
-@pytest.mark.parametrize("part", [256, 512])
+@pytest.mark.parametrize("part", [0, 256, 512])
 @pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [
     (1, 1, 32, 8, 128), (1, 0, 16, 8, 64), (1, 1, 16, 2, 256), (0, 0, 8, 2, 128), (2, 0, 8, 8, 64),
     (2, 1, 32, 8, 128), (0, 1, 4, 4, 256),
@@ -188,6 +188,16 @@ def test_decode_edge_lengths(stream, part, kv_dtype, q_dtype, Hq, Hkv, D):
     got, ref = run_decode(w, 55, stream, partition_size=part)
     check_close(got, ref, **tol_for(kv_dtype), what=f"edge lens kv={kv_dtype} D={D} G={Hq // Hkv}")
     assert np.all(got[0] == 0.0)  # context_len 0 -> zeros
+
+
+@pytest.mark.parametrize("part", [0, 4096])
+@pytest.mark.parametrize("kv_dtype", [1, 2])
+def test_decode_long_segments(stream, kv_dtype, part):
+    """Long rows: 256-block segments (64 blocks per wave), and more units than workgroups."""
+    w = wl.make_small(12 + kv_dtype, num_seqs=len(LONG_LENS), lens=LONG_LENS, Hq=16, Hkv=4, D=128,
+                      kv_dtype=kv_dtype, q_dtype=1)
+    got, ref = run_decode(w, 57, stream, partition_size=part)
+    check_close(got, ref, **tol_for(kv_dtype), what=f"long segments kv={kv_dtype} part={part}")
 
 
 def test_decode_invalid_block_ids_read_as_zero(stream):
@@ -203,12 +213,18 @@ def test_decode_invalid_block_ids_read_as_zero(stream):
 APPEND_LENS = [1, 2, 16, 17, 33, 100, 256, 257, 300, 513, 1000, 1024, 1025, 2000]
 
 
-@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,part", [
-    (1, 1, 32, 8, 128, 256), (1, 0, 16, 4, 64, 512), (2, 0, 32, 8, 128, 256), (2, 1, 8, 2, 256, 512),
-    (0, 0, 8, 8, 64, 256), (0, 1, 16, 4, 128, 512),
-])
-def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part):
-    w = wl.make_small(70 + D + kv_dtype, num_seqs=len(APPEND_LENS), lens=APPEND_LENS, Hq=Hq, Hkv=Hkv, D=D,
+# Long rows: segments of up to 256 blocks (64 per wave), the appended block at a late lane.
+LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000]
+
+
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,part,lens", [
+    (1, 1, 32, 8, 128, 0, APPEND_LENS), (1, 0, 16, 4, 64, 512, APPEND_LENS), (2, 0, 32, 8, 128, 0, APPEND_LENS),
+    (2, 1, 8, 2, 256, 512, APPEND_LENS), (0, 0, 8, 8, 64, 256, APPEND_LENS), (0, 1, 16, 4, 128, 512, APPEND_LENS),
+    (1, 1, 16, 4, 128, 256, APPEND_LENS), (1, 1, 8, 2, 128, 4096, LONG_LENS), (2, 1, 8, 2, 128, 0, LONG_LENS),
+], ids=["bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
+        "int8-long"])
+def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part, lens):
+    w = wl.make_small(70 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
                       kv_dtype=kv_dtype, q_dtype=q_dtype)
     inp = wl.numpy_inputs(w, 77)
     cfg = config_for(w, partition_size=part)
