@@ -1,19 +1,21 @@
 #!/usr/bin/env python3
-"""Paged-decode benchmark on one MI355X (the BASELINE.json metric).
+"""Paged-attention benchmark on one MI355X (the BASELINE.json metric, plus the other configurations).
 
-Step = one decode layer-step of the C2 configuration (Llama-3-8B layer shape: Hq=32, Hkv=8,
-D=128, bf16 KV, block 16, batch 64, contexts log-uniform in [128, 4096], shuffled physical
+Headline step = one decode layer-step of the C2 configuration (Llama-3-8B layer shape: Hq=32,
+Hkv=8, D=128, bf16 KV, block 16, batch 64, contexts log-uniform in [128, 4096], shuffled physical
 blocks): append the new token's K/V of every sequence into the paged cache and attend over each
-sequence's whole context, as one pa_paged_decode_append call (the fused kernel plus the split-K
-merge). Inputs are resident in HBM before timing starts; all launches go through the C-ABI of
-libpa_hip.so on one pa_stream and are timed with pa_events on that stream.
+sequence's whole context, as one pa_paged_decode_append call (the fused decode kernel plus the
+split-K merge). Inputs are resident in HBM before timing starts; all launches go through the
+C-ABI of libpa_hip.so on one pa_stream and are timed with pa_events recorded on that stream.
 
 Output: one JSON line. `value` is the achieved algorithmic HBM bandwidth of the whole step
 (distinct KV bytes read + Q + O + block tables + the appended K/V, divided by the step time);
-tokens/s per layer and us per layer-step ride along. `roofline` covers the same call; the
-two-call path (pa_kv_append + pa_paged_decode) is timed beside it for reference.
-`cpu_baseline` times the CPU oracle (a C restatement of the reference's StandardPagedAttentionKernel
-with its per-sequence decode loop) on a bounded sample of the same batch, on this host.
+tokens/s per layer and us per layer-step ride along. `roofline` covers the same call. `extra`
+times the other configurations the same way: C4 (int8 KV, fused append + decode), C5 (long
+contexts with a shared prefix, decode), C3 (mixed: fused decode of 48 sequences, the append of
+8 prefill chunks and their chunked prefill, with the prefill's MFMA rate). `cpu_baseline` times
+the CPU oracle (a C restatement of the reference's StandardPagedAttentionKernel with its
+per-sequence decode loop) on a bounded sample of the C2 batch, on this host.
 """
 from __future__ import annotations
 
@@ -33,6 +35,11 @@ import workloads as wl  # noqa: E402
 
 METRIC = "paged decode HBM GB/s (% peak) + tokens/s per layer, Llama-3-8B shape, 1 GPU"
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
+# HBM traffic of the headline call measured with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE per
+# dispatch, scaled by the same counters' reading for a plain copy of known size); written by the
+# profiling summary, absent until then.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_decode_append_traffic.json")
 
 
 def log(msg):
@@ -45,8 +52,18 @@ def bf16_trunc_torch(x):
     return (x.contiguous().view(torch.int32) >> 16).to(torch.int16)
 
 
+def tensor(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
 def make_inputs(w: wl.Workload, seed: int):
-    """Caches, q, new-token K/V and index arrays on the GPU (torch tensors as device memory)."""
+    """Caches, q, new-token K/V and index arrays on the GPU (torch tensors as device memory).
+
+    bf16/fp32 caches hold N(0,1) * value_scale values; int8 caches hold random codes in
+    [-127, 127] with per-(block, KV head) scales (absmax = 127 * scale), which is what the
+    kernels read whatever the codes' origin."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -58,18 +75,162 @@ def make_inputs(w: wl.Workload, seed: int):
     def randn(*shape):
         return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * vs
 
-    assert w.kv_dtype == pa.PA_DTYPE_BF16 and w.q_dtype == pa.PA_DTYPE_BF16
-    k_cache = bf16_trunc_torch(randn(nb, Hkv, 16, D))
-    v_cache = bf16_trunc_torch(randn(nb, Hkv, 16, D))
-    q = bf16_trunc_torch(randn(S, Hq, D))
-    k_new = bf16_trunc_torch(randn(S, Hkv, D))
-    v_new = bf16_trunc_torch(randn(S, Hkv, D))
-    # The new token of sequence s sits at position context_len - 1.
-    pos = w.context_lens.astype(np.int64) - 1
-    slots = w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    return dict(k_cache=k_cache, v_cache=v_cache, q=q, k_new=k_new, v_new=v_new,
-                slots=t(slots), tables=t(w.block_tables), lens=t(w.context_lens))
+    def act(*shape):  # activations in the q dtype
+        x = randn(*shape)
+        return bf16_trunc_torch(x) if w.q_dtype == pa.PA_DTYPE_BF16 else x
+
+    out = dict(q=act(S, Hq, D), k_new=act(S, Hkv, D), v_new=act(S, Hkv, D),
+               tables=tensor(w.block_tables), lens=tensor(w.context_lens),
+               k_scale=None, v_scale=None, k_absmax=None, v_absmax=None)
+    if w.kv_dtype == pa.PA_DTYPE_INT8:
+        for n in ("k", "v"):
+            out[f"{n}_cache"] = torch.randint(-127, 128, (nb, Hkv, 16, D), generator=g, device=dev,
+                                              dtype=torch.int8)
+            sc = torch.rand(nb, Hkv, generator=g, device=dev, dtype=torch.float32) * 0.02 + 0.01
+            out[f"{n}_scale"] = sc
+            out[f"{n}_absmax"] = sc * 127.0
+    elif w.kv_dtype == pa.PA_DTYPE_BF16:
+        out["k_cache"] = bf16_trunc_torch(randn(nb, Hkv, 16, D))
+        out["v_cache"] = bf16_trunc_torch(randn(nb, Hkv, 16, D))
+    else:
+        out["k_cache"] = randn(nb, Hkv, 16, D)
+        out["v_cache"] = randn(nb, Hkv, 16, D)
+    return out
+
+
+def config_of(w: wl.Workload, partition_size=0):
+    return pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                          kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks,
+                          partition_size=partition_size)
+
+
+class Timer:
+    """Times a callable with pa_events recorded on the stream the library launches on."""
+
+    def __init__(self, dev, stream):
+        self.dev, self.stream = dev, stream
+
+    def __call__(self, fn, steps, warmup):
+        import torch
+
+        for _ in range(warmup):
+            fn()
+        self.stream.synchronize()
+        e0, e1 = pa.Event(self.dev), pa.Event(self.dev)
+        torch.cuda.synchronize()
+        e0.record(self.stream)
+        for _ in range(steps):
+            fn()
+        e1.record(self.stream)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / steps
+        e0.destroy()
+        e1.destroy()
+        return ms
+
+
+def decode_step(w, inp, stream, cfg, fused, out, ws, wsb):
+    S, mcl = w.num_seqs, w.max_context_len
+    if fused:
+        return lambda: pa.paged_decode_append(stream, cfg, out, inp["q"], inp["k_new"], inp["v_new"], inp["k_cache"],
+                                              inp["v_cache"], inp["k_scale"], inp["v_scale"], inp["k_absmax"],
+                                              inp["v_absmax"], inp["tables"], inp["lens"], S, w.max_blocks, mcl,
+                                              ws, wsb)
+    return lambda: pa.paged_decode(stream, cfg, out, inp["q"], inp["k_cache"], inp["v_cache"], inp["k_scale"],
+                                   inp["v_scale"], inp["tables"], inp["lens"], S, w.max_blocks, mcl, ws, wsb)
+
+
+def decode_buffers(w, cfg):
+    import torch
+
+    out = torch.empty((w.num_seqs, w.num_q_heads, w.head_dim), dtype=torch.float32, device="cuda:0")
+    wsb = pa.decode_workspace_size(cfg, w.num_seqs, w.max_context_len)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device="cuda:0")
+    return out, ws, wsb
+
+
+def append_bytes(w):
+    """The appended token of every sequence: new K/V read in the activation dtype + cache write."""
+    act = 2 if w.q_dtype == pa.PA_DTYPE_BF16 else 4
+    cache = {0: 4, 1: 2, 2: 1}[w.kv_dtype]
+    return 2 * w.num_seqs * w.num_kv_heads * w.head_dim * (act + cache)
+
+
+def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
+    inp = make_inputs(w, seed)
+    cfg = config_of(w)
+    out, ws, wsb = decode_buffers(w, cfg)
+    ms = timer(decode_step(w, inp, stream, cfg, fused, out, ws, wsb), steps, warmup)
+    nbytes = w.decode_algorithmic_bytes() + (append_bytes(w) if fused else 0)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    res = {"us_per_layer_step": round(ms * 1e3, 3), "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1),
+           "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "tokens_per_s_per_layer": round(w.num_seqs / (ms * 1e-3), 1),
+           "context_tokens": int(w.context_lens.sum()), "num_seqs": w.num_seqs,
+           "step": "pa_paged_decode_append" if fused else "pa_paged_decode"}
+    del inp, out, ws
+    return res
+
+
+def run_c3(timer, stream, steps, warmup, seed):
+    """C3: fused decode of 48 sequences + append of 8 prefill chunks (512 tokens each) + their prefill."""
+    import torch
+
+    w = wl.make_c3()
+    inp = make_inputs(w, seed)
+    cfg = config_of(w)
+    out, ws, wsb = decode_buffers(w, cfg)
+    dec = decode_step(w, inp, stream, cfg, True, out, ws, wsb)
+
+    P = w.prefill_prefix.astype(np.int64)
+    L = w.prefill_chunk
+    n_pre = len(P)
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(seed + 1)
+    tot = n_pre * L
+    q_pre = bf16_trunc_torch(torch.randn(tot, w.num_q_heads, w.head_dim, generator=g, device="cuda:0") * 0.5)
+    k_pre = bf16_trunc_torch(torch.randn(tot, w.num_kv_heads, w.head_dim, generator=g, device="cuda:0") * 0.5)
+    v_pre = bf16_trunc_torch(torch.randn(tot, w.num_kv_heads, w.head_dim, generator=g, device="cuda:0") * 0.5)
+    pos = (P[:, None] + np.arange(L)[None, :])
+    tab = w.prefill_tables
+    slots = (tab[np.arange(n_pre)[:, None], pos // 16].astype(np.int64) * 16 + pos % 16).reshape(-1)
+    slots_g = tensor(slots)
+    q_start = tensor(np.arange(n_pre + 1, dtype=np.int32) * L)
+    prefix_g = tensor(P.astype(np.int32))
+    tab_g = tensor(tab)
+    out_pre = torch.empty((tot, w.num_q_heads, w.head_dim), dtype=torch.float32, device="cuda:0")
+
+    def app():
+        pa.kv_append(stream, cfg, k_pre, v_pre, slots_g, tot, inp["k_cache"], inp["v_cache"])
+
+    def pre():
+        pa.chunked_prefill(stream, cfg, out_pre, q_pre, q_start, prefix_g, inp["k_cache"], inp["v_cache"], None,
+                           None, tab_g, n_pre, tab.shape[1], L)
+
+    def step():
+        dec()
+        app()
+        pre()
+
+    ms_dec = timer(dec, steps, warmup)
+    ms_app = timer(app, steps, warmup)
+    ms_pre = timer(pre, steps, warmup)
+    ms_step = timer(step, steps, warmup)
+    flops = float(4 * w.num_q_heads * w.head_dim * np.sum(L * P + L * (L + 1) / 2))
+    pre_kv_bytes = float(np.sum(P + L)) * w.kv_bytes_per_token()
+    dec_bytes = w.decode_algorithmic_bytes() + append_bytes(w)
+    app_bytes = tot * w.num_kv_heads * w.head_dim * 2 * (2 + 2)
+    tflops = flops / (ms_pre * 1e-3) / 1e12
+    return {
+        "us_per_layer_step": round(ms_step * 1e3, 3),
+        "decode": {"us": round(ms_dec * 1e3, 3), "num_seqs": w.num_seqs, "algorithmic_bytes": int(dec_bytes),
+                   "gbps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
+                   "frac_hbm": round(dec_bytes / (ms_dec * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)},
+        "chunk_append": {"us": round(ms_app * 1e3, 3), "tokens": tot, "algorithmic_bytes": int(app_bytes),
+                         "gbps": round(app_bytes / (ms_app * 1e-3) / 1e9, 1)},
+        "prefill": {"us": round(ms_pre * 1e3, 3), "chunks": n_pre, "chunk_len": L,
+                    "prefix_lens": [int(x) for x in P], "flops": flops, "tflops": round(tflops, 1),
+                    "frac_mfma_bf16_dense": round(tflops / PEAK_BF16_TFLOPS, 4), "kv_bytes": int(pre_kv_bytes)},
+    }
 
 
 def cpu_baseline(w: wl.Workload, inp, budget_s: float):
@@ -78,21 +239,18 @@ def cpu_baseline(w: wl.Workload, inp, budget_s: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pa_oracle as orc  # test infrastructure: the timed CPU baseline only
 
-    cfg = pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
-                         kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks)
+    cfg = config_of(w)
     kc = inp["k_cache"].cpu().numpy().view(np.uint16)
     vc = inp["v_cache"].cpu().numpy().view(np.uint16)
     q = inp["q"].cpu().numpy().view(np.uint16)
-    order = np.arange(w.num_seqs)
     n, spent, toks = 0, 0.0, 0
     t_start = time.perf_counter()
     while n < w.num_seqs and spent < budget_s:
-        s = order[n]
         t0 = time.perf_counter()
-        orc.paged_decode(cfg, np.ascontiguousarray(q[s:s + 1]), kc, vc, None, None,
-                         w.block_tables[s:s + 1], w.context_lens[s:s + 1], n_threads=1)
+        orc.paged_decode(cfg, np.ascontiguousarray(q[n:n + 1]), kc, vc, None, None,
+                         w.block_tables[n:n + 1], w.context_lens[n:n + 1], n_threads=1)
         spent += time.perf_counter() - t0
-        toks += int(w.context_lens[s])
+        toks += int(w.context_lens[n])
         n += 1
     wall = time.perf_counter() - t_start
     full_time = spent * (int(w.context_lens.sum()) / max(toks, 1))
@@ -138,6 +296,15 @@ def _cpu_model():
     return "unknown"
 
 
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return float(t["hbm_bytes_per_call"]), t
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,7 +315,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="budget of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--only-step", action="store_true",
-                    help="time the fused step only (no two-call comparison, no CPU baseline): for profiling")
+                    help="time the headline step only (no two-call comparison, no other configurations, no "
+                         "CPU baseline): for profiling")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 measurements")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run 10 plain device-to-device copies of this many MiB through pa_memcpy, the "
                          "reference kernel for scaling hardware byte counters")
@@ -172,47 +341,40 @@ def main():
     dev = pa.Device(0)
     props = dev.props()
     stream = pa.Stream(dev)
-    cfg = pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
-                         kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks,
-                         partition_size=args.partition_size)
-    S, mcl = w.num_seqs, w.max_context_len
-    out = torch.empty((S, w.num_q_heads, w.head_dim), dtype=torch.float32, device="cuda:0")
-    wsb = pa.decode_workspace_size(cfg, S, mcl)
-    ws = torch.zeros((max(wsb, 1),), dtype=torch.uint8, device="cuda:0")  # zero-filled once
-    torch.cuda.synchronize()
-
-    def step():
-        pa.paged_decode_append(stream, cfg, out, inp["q"], inp["k_new"], inp["v_new"], inp["k_cache"],
-                               inp["v_cache"], None, None, None, None, inp["tables"], inp["lens"], S,
-                               w.max_blocks, mcl, ws, wsb)
+    timer = Timer(dev, stream)
+    cfg = config_of(w, args.partition_size)
+    S = w.num_seqs
+    out, ws, wsb = decode_buffers(w, cfg)
+    step = decode_step(w, inp, stream, cfg, True, out, ws, wsb)
 
     def two_call_step():
         pa.kv_append(stream, cfg, inp["k_new"], inp["v_new"], inp["slots"], S, inp["k_cache"], inp["v_cache"])
         pa.paged_decode(stream, cfg, out, inp["q"], inp["k_cache"], inp["v_cache"], None, None,
-                        inp["tables"], inp["lens"], S, w.max_blocks, mcl, ws, wsb)
+                        inp["tables"], inp["lens"], S, w.max_blocks, w.max_context_len, ws, wsb)
 
-    def timed(fn, n):
-        e0, e1 = pa.Event(dev), pa.Event(dev)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        ms = e0.elapsed_ms(e1) / n
-        e0.destroy()
-        e1.destroy()
-        return ms
-
-    for _ in range(args.warmup):
-        step()
-    stream.synchronize()
-    step_ms = timed(step, args.steps)
+    step_ms = timer(step, args.steps, args.warmup)
     two_call_ms = float("nan")
+    extra = None
     if not args.only_step:
-        for _ in range(args.warmup):
-            two_call_step()
-        two_call_ms = timed(two_call_step, args.steps)
+        pos = w.context_lens.astype(np.int64) - 1
+        inp["slots"] = tensor(w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16)
+        two_call_ms = timer(two_call_step, args.steps, args.warmup)
+        log(f"[bench] C2 fused step {step_ms * 1e3:.2f} us, two-call step {two_call_ms * 1e3:.2f} us")
+        if not args.no_extra:
+            extra = {}
+            n = max(20, args.steps // 2)
+            extra["C4"] = run_decode_config(wl.make_c4(), timer, stream, n, args.warmup, True, 4)
+            log(f"[bench] C4 {extra['C4']['us_per_layer_step']} us")
+            w5 = wl.make_c5()
+            c5 = run_decode_config(w5, timer, stream, n, args.warmup, False, 5)
+            logical = float(w5.context_lens.sum()) * w5.kv_bytes_per_token()
+            c5["logical_kv_bytes"] = int(logical)
+            c5["logical_gbps"] = round(logical / (c5["us_per_layer_step"] * 1e-6) / 1e9, 1)
+            extra["C5"] = c5
+            log(f"[bench] C5 {c5['us_per_layer_step']} us")
+            extra["C3"] = run_c3(timer, stream, n, args.warmup, 3)
+            log(f"[bench] C3 {extra['C3']['us_per_layer_step']} us")
+            torch.cuda.empty_cache()
     torch.cuda.synchronize()
     if args.copy_calibration_mb > 0:
         nbytes = args.copy_calibration_mb << 20
@@ -222,14 +384,11 @@ def main():
             pa.call("pa_memcpy", dst.data_ptr(), src.data_ptr(), nbytes, pa.PA_MEMCPY_DEVICE_TO_DEVICE, stream.handle)
         stream.synchronize()
         log(f"[bench] copy calibration: 10 x {nbytes} bytes device-to-device")
-    log(f"[bench] fused step {step_ms * 1e3:.2f} us, two-call step {two_call_ms * 1e3:.2f} us")
 
     dec_bytes = w.decode_algorithmic_bytes()
-    # the appended token: new K/V read (bf16) + written into the cache
-    app_bytes = 2 * S * w.num_kv_heads * w.head_dim * 2 * 2
-    step_bytes = dec_bytes + app_bytes
+    step_bytes = dec_bytes + append_bytes(w)
     value = step_bytes / (step_ms * 1e-3) / 1e9
-    achieved = value
+    traffic, traffic_src = load_traffic()
 
     cpu = None
     if args.cpu_seconds > 0 and not args.only_step:
@@ -261,17 +420,20 @@ def main():
         "tokens_per_s_per_layer": round(S / (step_ms * 1e-3), 1),
         "us_per_layer_step": round(step_ms * 1e3, 3),
         "roofline": {
-            "kernel": "pa_paged_decode_append (fused append + paged decode kernel, then split-K merge)",
+            "kernel": "pa_paged_decode_append call: paged_decode_mfma_persistent_kernel<128, bf16, bf16 q, "
+                      "append> + paged_decode_merge_split_kernel<128>",
             "bound": "hbm",
-            "achieved": round(achieved, 2),
+            "achieved": round(value, 2),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "frac": round(value / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": int(step_bytes),
             "us_per_launch": round(step_ms * 1e3, 3),
         },
         "two_call_us_per_layer_step": None if two_call_ms != two_call_ms else round(two_call_ms * 1e3, 3),
+        "extra": extra,
         "cpu_baseline": cpu,
         "device": {"name": props.name.decode(), "arch": props.arch.decode(), "cus": props.compute_units},
     }

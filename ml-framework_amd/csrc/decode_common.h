@@ -181,14 +181,18 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
 // Range length (blocks) of the MFMA kernel's split of the `total` blocks of all sequences (one KV
 // head's worth); the decode and the merge kernel derive the same value from the same arguments.
 // By default the split_grid workgroups form split_grid / Hkv ranges, each range done by Hkv
-// workgroups, one per KV head; ranges hold 4 to 256 blocks (more ranges than workgroups when
-// 256 is not enough: workgroups then walk several units).
+// workgroups, one per KV head; ranges hold 4 to 256 blocks (when 256 is not enough, workgroups
+// walk k units each).
 __device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64_t total) {
     if (a.split_blocks > 0) return a.split_blocks;
     const int64_t nr = a.split_grid >= a.num_kv_heads ? a.split_grid / a.num_kv_heads : 1;
-    int64_t c = (total + nr - 1) / nr;
+    // k rounds of nr ranges each, k the fewest that keeps ranges within 256 blocks (a wave's block
+    // ids fit one VGPR); the ranges of the last round are as long as the others', so no workgroup
+    // gets a whole extra range.
+    const int64_t k = (total + 256 * nr - 1) / (256 * nr);
+    int64_t c = (total + k * nr - 1) / (k * nr);
     c = (c + 3) & ~static_cast<int64_t>(3);
-    return c < 4 ? 4 : (c > 256 ? 256 : c);  // 256: a wave's block ids fit one VGPR
+    return c < 4 ? 4 : c;
 }
 
 // Merge pass of the MFMA kernel: one workgroup per (KV head, sequence). Sequence seq occupies
