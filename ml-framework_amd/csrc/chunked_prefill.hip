@@ -8,13 +8,15 @@
 // (ContinuousBatching/Prefill/PrefillHandler.cs:85-89, PrefillConfiguration.cs:21); each chunk is
 // one call here.
 //
-// Work decomposition: one workgroup per (16-query tile, KV head, sequence); wave w handles query
-// head w (w + 4, ...) of the KV head's group, so the group's 4 waves read the same K/V tiles
-// (HBM once, L1/L2 after). Per 16-key block: S^T[16 keys][16 queries] = K . Q^T on
-// v_mfma_f32_16x16x32_bf16, online softmax per query in fp32 with the causal limit per query,
-// O[16 queries][D] += P . V on v_mfma_f32_16x16x16_bf16 with P split into bf16 high and low parts.
-// These are the decode kernel's operand layouts with the 16 MFMA rows holding 16 queries instead
-// of (padded) heads.
+// Work decomposition: one workgroup per (16-query tile, KV head, sequence). Its 4 waves split the
+// key blocks (wave w takes blocks w, w + 4, ...) and each wave runs every query head of the KV
+// head's group on each block it loads (HG heads per pass), so a K/V tile is read from memory once
+// per workgroup and each loaded operand feeds HG heads' MFMAs. Per 16-key block and head:
+// S^T[16 keys][16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16, online softmax per query in fp32
+// with the causal limit per query, O[16 queries][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
+// split into bf16 high and low parts. These are the decode kernel's operand layouts with the 16
+// MFMA rows holding 16 queries instead of (padded) heads. The 4 waves' (max, sum, O) are combined
+// through LDS at the end, head by head.
 #include <string>
 
 #include "decode_common.h"
@@ -42,8 +44,11 @@ struct PrefillArgs {
 
 constexpr float kPrefillRescaleThreshold = 8.0f;
 
-template <int D, int KV, bool QF32>
-__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(const PrefillArgs a) {
+// Heads per pass: bounded by the accumulators (HG x D / 16 x 4 registers) and Q operands.
+template <int D, bool QF32> constexpr int prefill_heads_per_pass() { return D > 128 ? 1 : (QF32 ? 2 : 4); }
+
+template <int D, int KV, bool QF32, int HG>
+__global__ __launch_bounds__(256, 1) void chunked_prefill_kernel(const PrefillArgs a) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;
@@ -51,6 +56,8 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
     constexpr int TILE = 16 * D;
     using KR = typename Raw::K;
     using VR = typename Raw::V;
+    __shared__ float s_m[4][HG][16], s_l[4][HG][16];
+    __shared__ float s_x[2][D][16];
 
     const int qt = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const int lane = threadIdx.x & 63;
@@ -64,11 +71,11 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
     const int i0 = qt * 16;
     if (i0 >= Lc) return;
     const int nq = min(16, Lc - i0);
-    int T = P + Lc;
-    T = min(T, a.max_blocks_per_seq * 16);
+    const int T = min(P + Lc, a.max_blocks_per_seq * 16);
     const bool causal = a.mask_mode == 0 || (a.mask_mode == 1 && P > 0);
     const int kmax = causal ? min(T, P + i0 + nq) : T;  // keys any query of the tile may see
     const int nkb = (kmax + 15) / 16;
+    const int nb = nkb > wave ? (nkb - wave + 3) / 4 : 0;  // this wave's blocks: wave + 4j
     // this lane's query (column n of S^T) sees keys [0, klim)
     const bool qvalid = n < nq;
     const int klim = causal ? min(T, P + i0 + n + 1) : T;
@@ -79,11 +86,12 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
     const int k_lane_off = (n * D + 8 * q4) * ELT;
     const int v_lane_off = (n * 16 + 4 * q4) * ELT;
 
-    for (int g = wave; g < G; g += 4) {
-        const int head = kvh * G + g;
-        // Q^T operand: lane (q4, n) holds query i0 + n of this head, dims 32s + 8q4 .. +8.
-        bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
-        {
+    for (int g0 = 0; g0 < G; g0 += HG) {
+        // Q^T operands: lane (q4, n) holds query i0 + n of head kvh*G + g0 + h, dims 32s + 8q4 .. +8.
+        bf16x8_t qhi[HG][NSLAB], qlo[QF32 ? HG : 1][QF32 ? NSLAB : 1];
+#pragma unroll
+        for (int h = 0; h < HG; h++) {
+            const int head = kvh * G + g0 + h;
             const int64_t qrow = (static_cast<int64_t>(q0 + i0 + (qvalid ? n : 0)) * Hq + head) * D;
 #pragma unroll
             for (int s = 0; s < NSLAB; s++) {
@@ -93,55 +101,33 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
                     float x[8];
 #pragma unroll
                     for (int e = 0; e < 8; e++) x[e] = qvalid ? qp[e] : 0.0f;
-                    uint32_t h[4], l[4];
+                    uint32_t hh[4], ll[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        h[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
+                        hh[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
                         const float r0 = x[2 * e] - __uint_as_float(__float_as_uint(x[2 * e]) & 0xffff0000u);
                         const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
-                        l[e] = pack_bf16_trunc(r0, r1);
+                        ll[e] = pack_bf16_trunc(r0, r1);
                     }
-                    qhi[s] = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
-                    qlo[s] = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+                    qhi[h][s] = __builtin_bit_cast(bf16x8_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+                    qlo[h][s] = __builtin_bit_cast(bf16x8_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
                 } else {
                     const uint4 raw = qvalid
                         ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
                         : make_uint4(0, 0, 0, 0);
-                    qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
+                    qhi[h][s] = __builtin_bit_cast(bf16x8_t, raw);
                 }
             }
         }
 
-        // Block ids (and int8 scales), 64 at a time: lane j holds key block c0 + j.
-        int bid_chunk = -1, c0 = -64;
-        float ks_chunk = 0.0f, vs_chunk = 0.0f;
-        auto refresh = [&](int lb) {
-            c0 = lb & ~63;
-            const int lbj = c0 + lane;
-            int id = -1;
-            if (lbj < nkb) {
-                id = table[lbj];
-                if (id >= a.num_blocks) id = -1;
-            }
-            bid_chunk = id;
-            if constexpr (KV == PA_DTYPE_INT8) {
-                ks_chunk = id >= 0 ? a.k_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
-                vs_chunk = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
-            }
-        };
-        auto block_id = [&](int lb) -> int {
-            if (lb >= nkb) return -1;
-            if ((lb & ~63) != c0) refresh(lb);
-            return __builtin_amdgcn_readlane(bid_chunk, lb & 63);
-        };
-        // the int8 scales of block lb are taken here, with its id: the 2-block look-ahead may
-        // move the 64-block window before block lb is consumed
-        auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], float (&kvs)[2], int lb) {
-            const int bid = block_id(lb);
-            if constexpr (KV == PA_DTYPE_INT8) {
-                kvs[0] = readlane_f(ks_chunk, lb & 63);
-                kvs[1] = readlane_f(vs_chunk, lb & 63);
-            }
+        // This wave's key blocks go in windows of 64: lane j holds the id (and int8 scales) of
+        // block wave + 4 (w0 + j), loaded once per window, so the streaming loop issues only the
+        // K/V loads (a table load inside it would make the wave wait for every load before it).
+        int my_bid = -1;
+        float my_ks = 0.0f, my_vs = 0.0f;
+        auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j, int nbw) {
+            int bid = j < nbw ? __builtin_amdgcn_readlane(my_bid, j) : -1;
+            bid = bid < a.num_blocks ? bid : -1;
             const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
             const int bytes = bid >= 0 ? TILE * ELT : 0;
             const __amdgpu_buffer_rsrc_t rk =
@@ -154,115 +140,200 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
             for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
         };
 
-        float m_run = -INFINITY, l_run = 0.0f;
-        f32x4_t acc[NT];
+        float m_run[HG], l_run[HG];
+        f32x4_t acc[HG][NT];
 #pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h = 0; h < HG; h++) {
+            m_run[h] = -INFINITY;
+            l_run[h] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[h][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 
-        auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], const float (&kvs)[2], int lb) {
-            f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int sl = 0; sl < NSLAB; sl++) {
-                const bf16x8_t kop = k_operand(kr[sl]);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
-                if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
-            }
+        auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], int j, int lb) {
             float ks = 1.0f, vfac = 1.0f;
-            if constexpr (KV == PA_DTYPE_INT8) {
-                ks = kvs[0];
-                vfac = kvs[1];
+            if constexpr (KV == PA_DTYPE_INT8) {  // an invalid block's tile reads as zeros, scale 0
+                const int bid = __builtin_amdgcn_readlane(my_bid, j);
+                const bool ok = bid >= 0 && bid < a.num_blocks;
+                ks = ok ? readlane_f(my_ks, j) : 0.0f;
+                vfac = ok ? readlane_f(my_vs, j) : 0.0f;
             }
+            bf16x8_t kop[NSLAB];
+#pragma unroll
+            for (int sl = 0; sl < NSLAB; sl++) kop[sl] = k_operand(kr[sl]);
+            s16x4_t vop[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) vop[t] = v_operand(vr[t]);
             const int kbase = lb * 16 + 4 * q4;
-            float sc[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float v = s[i];
-                if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
-                v = v * a.scale;
-                // queries past the tile keep finite scores (their rows are never stored)
-                sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
-            }
-            const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            const bool grow = bm > m_run + kPrefillRescaleThreshold;
-            if (__any(grow)) {
-                const float m_new = grow ? bm : m_run;
-                const float alpha = __expf(m_run - m_new);
-                l_run *= alpha;
-                m_run = m_new;
-                float ar[4];
+            for (int h = 0; h < HG; h++) {
+                f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
+                for (int sl = 0; sl < NSLAB; sl++) {
+                    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qhi[h][sl], s, 0, 0, 0);
+                    if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qlo[h][sl], s, 0, 0, 0);
+                }
+                float sc[4];
 #pragma unroll
-                for (int t = 0; t < NT; t++)
+                for (int i = 0; i < 4; i++) {
+                    float v = s[i];
+                    if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
+                    v = v * a.scale;
+                    // queries past the tile keep finite scores (their rows are never stored)
+                    sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
+                }
+                const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+                const bool grow = bm > m_run[h] + kPrefillRescaleThreshold;
+                if (__any(grow)) {
+                    const float m_new = grow ? bm : m_run[h];
+                    // 0 from -inf; 1 for a query whose max stays -inf (nothing accumulated yet)
+                    const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run[h] - m_new);
+                    l_run[h] *= alpha;
+                    m_run[h] = m_new;
+                    float ar[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[t][i] *= ar[i];
-            }
-            float p[4];
+                    for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                p[i] = __expf(sc[i] - m_run);
-                l_run += p[i];
-                if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
-            }
-            uint32_t hi[2], lo[2];
+                    for (int t = 0; t < NT; t++)
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const float a0 = p[2 * e], a1 = p[2 * e + 1];
-                const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
-                const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
-                hi[e] = pack_bf16_trunc(a0, a1);
-                lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
-            }
-            const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
-            const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+                        for (int i = 0; i < 4; i++) acc[h][t][i] *= ar[i];
+                }
+                // A wave sees only every 4th block: all of them may be masked for a query, whose
+                // max then stays -inf; its probabilities are 0, not exp(-inf + inf).
+                float p[4];
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const s16x4_t vop = v_operand(vr[t]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+                for (int i = 0; i < 4; i++) {
+                    p[i] = sc[i] == -INFINITY ? 0.0f : __expf(sc[i] - m_run[h]);
+                    l_run[h] += p[i];
+                    if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
+                }
+                uint32_t hi[2], lo[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const float a0 = p[2 * e], a1 = p[2 * e + 1];
+                    const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+                    const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+                    hi[e] = pack_bf16_trunc(a0, a1);
+                    lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+                }
+                const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+                const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[h][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop[t], acc[h][t], 0, 0, 0);
+                    acc[h][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop[t], acc[h][t], 0, 0, 0);
+                }
             }
         };
 
-        {
+        for (int w0 = 0; w0 < nb; w0 += 64) {
+            const int nbw = min(64, nb - w0);
+            my_bid = lane < nbw ? table[wave + 4 * (w0 + lane)] : -1;
+            if constexpr (KV == PA_DTYPE_INT8) {  // unconditional loads (index clamped)
+                const int sb = my_bid >= 0 && my_bid < a.num_blocks ? my_bid : 0;
+                my_ks = a.k_scale[static_cast<int64_t>(sb) * Hkv + kvh];
+                my_vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + kvh];
+            }
             KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
             VR va[NT], vb[NT], vx[NT];
-            float sa[2] = {1.0f, 1.0f}, sb[2] = {1.0f, 1.0f}, sx[2] = {1.0f, 1.0f};
             int j = 0;
-            load(ka, va, sa, 0);
-            load(kb, vb, sb, 1);
-            while (j < nkb) {
-                load(kx, vx, sx, j + 2);
-                compute(ka, va, sa, j);
-                if (++j >= nkb) break;
-                load(ka, va, sa, j + 2);
-                compute(kb, vb, sb, j);
-                if (++j >= nkb) break;
-                load(kb, vb, sb, j + 2);
-                compute(kx, vx, sx, j);
+            load(ka, va, 0, nbw);
+            load(kb, vb, 1, nbw);
+            while (j < nbw) {
+                load(kx, vx, j + 2, nbw);
+                compute(ka, va, j, wave + 4 * (w0 + j));
+                if (++j >= nbw) break;
+                load(ka, va, j + 2, nbw);
+                compute(kb, vb, j, wave + 4 * (w0 + j));
+                if (++j >= nbw) break;
+                load(kb, vb, j + 2, nbw);
+                compute(kx, vx, j, wave + 4 * (w0 + j));
                 ++j;
             }
         }
 
-        // rows of acc are queries 4q4 + i; their sums live in lanes (any q4, n = 4q4 + i)
-        const float l_tot = rows_sum(l_run);
+        // ---- combine the 4 waves per head: weights exp(m_w - M), then a 2-level tree in LDS ----
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int qi = 4 * q4 + i;
-            const float li = __shfl(l_tot, qi, 64);
-            if (qi < nq) {
-                const float inv = 1.0f / li;
-                float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
-#pragma unroll
-                for (int t = 0; t < NT; t++) o[16 * t + n] = acc[t][i] * inv;
+        for (int h = 0; h < HG; h++) {
+            const float l_tot = rows_sum(l_run[h]);
+            if (q4 == 0) {
+                s_m[wave][h][n] = m_run[h];
+                s_l[wave][h][n] = l_tot;
             }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < HG; h++) {
+            float M[4], f_own[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = 4 * q4 + i;
+                M[i] = fmaxf(fmaxf(s_m[0][h][r], s_m[1][h][r]), fmaxf(s_m[2][h][r], s_m[3][h][r]));
+                // 0 for a wave that saw no unmasked key of query r (or no block at all)
+                f_own[i] = s_m[wave][h][r] == -INFINITY ? 0.0f : __expf(s_m[wave][h][r] - M[i]);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[h][t][i] *= f_own[i];
+            if (wave >= 2) {
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    *reinterpret_cast<f32x4_t*>(&s_x[wave - 2][16 * t + n][4 * q4]) = acc[h][t];
+            }
+            __syncthreads();
+            if (wave < 2) {
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    f32x4_t* slot = reinterpret_cast<f32x4_t*>(&s_x[wave][16 * t + n][4 * q4]);
+                    acc[h][t] += *slot;
+                    if (wave == 1) *slot = acc[h][t];
+                }
+            }
+            __syncthreads();
+            if (wave == 0) {
+                float L[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * q4 + i;
+                    L[i] = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < 4; w++)
+                        L[i] += s_m[w][h][r] == -INFINITY ? 0.0f : s_l[w][h][r] * __expf(s_m[w][h][r] - M[i]);
+                }
+                const int head = kvh * G + g0 + h;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int qi = 4 * q4 + i;
+                    if (qi < nq) {
+                        const float inv = 1.0f / L[i];
+                        float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            const f32x4_t other = *reinterpret_cast<const f32x4_t*>(&s_x[1][16 * t + n][4 * q4]);
+                            o[16 * t + n] = (acc[h][t][i] + other[i]) * inv;
+                        }
+                    }
+                }
+            }
+            __syncthreads();  // s_x reuse by the next head
         }
     }
 }
 
 template <int D, int KV>
 void launch(const PrefillArgs& a, bool qf32, dim3 grid, hipStream_t s) {
-    if (qf32) chunked_prefill_kernel<D, KV, true><<<grid, 256, 0, s>>>(a);
-    else chunked_prefill_kernel<D, KV, false><<<grid, 256, 0, s>>>(a);
+    // the heads per pass must divide the group; other group sizes run one head per pass
+    if (qf32) {
+        constexpr int HG = prefill_heads_per_pass<D, true>();
+        if (a.group % HG == 0) chunked_prefill_kernel<D, KV, true, HG><<<grid, 256, 0, s>>>(a);
+        else chunked_prefill_kernel<D, KV, true, 1><<<grid, 256, 0, s>>>(a);
+    } else {
+        constexpr int HG = prefill_heads_per_pass<D, false>();
+        if (a.group % HG == 0) chunked_prefill_kernel<D, KV, false, HG><<<grid, 256, 0, s>>>(a);
+        else if (HG > 2 && a.group % 2 == 0) chunked_prefill_kernel<D, KV, false, (HG > 2 ? 2 : 1)><<<grid, 256, 0, s>>>(a);
+        else chunked_prefill_kernel<D, KV, false, 1><<<grid, 256, 0, s>>>(a);
+    }
 }
 
 template <int D>
