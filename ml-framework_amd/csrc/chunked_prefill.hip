@@ -8,15 +8,17 @@
 // (ContinuousBatching/Prefill/PrefillHandler.cs:85-89, PrefillConfiguration.cs:21); each chunk is
 // one call here.
 //
-// Work decomposition: one workgroup per (16-query tile, KV head, sequence). Its 4 waves split the
-// key blocks (wave w takes blocks w, w + 4, ...) and each wave runs every query head of the KV
-// head's group on each block it loads (HG heads per pass), so a K/V tile is read from memory once
-// per workgroup and each loaded operand feeds HG heads' MFMAs. Per 16-key block and head:
+// Work decomposition: one workgroup per (16-query tile, KV head, sequence); wave w computes query
+// head w (w + 4, ...) of the KV head's group. The workgroup streams the key blocks through LDS:
+// each thread loads its 16-byte pieces of a block's K and V tiles into registers R blocks ahead,
+// writes them into one of two LDS slots, and after one barrier every wave reads its MFMA operands
+// from that slot. A K/V tile thus crosses from memory once per workgroup and R blocks are in
+// flight per workgroup. The LDS tiles are stored with an XOR swizzle of 16-byte chunks so the
+// operand reads are free of bank conflicts. Per 16-key block and head:
 // S^T[16 keys][16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16, online softmax per query in fp32
 // with the causal limit per query, O[16 queries][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
 // split into bf16 high and low parts. These are the decode kernel's operand layouts with the 16
-// MFMA rows holding 16 queries instead of (padded) heads. The 4 waves' (max, sum, O) are combined
-// through LDS at the end, head by head.
+// MFMA rows holding 16 queries instead of (padded) heads.
 #include <string>
 
 #include "decode_common.h"
@@ -44,11 +46,24 @@ struct PrefillArgs {
 
 constexpr float kPrefillRescaleThreshold = 8.0f;
 
-// Heads per pass: bounded by the accumulators (HG x D / 16 x 4 registers) and Q operands.
-template <int D, bool QF32> constexpr int prefill_heads_per_pass() { return D > 128 ? 1 : (QF32 ? 2 : 4); }
+// LDS geometry of one staged block (K tile then V tile) for head_dim D and element size ELT.
+template <int D, int ELT> struct PrefillTile {
+    static constexpr int RC = D * ELT / 16;             // 16-byte chunks per K row
+    static constexpr int K_CHUNKS = 16 * RC;             // K tile [16][D]
+    static constexpr int VRC = ELT;                      // 16-byte chunks per V row (16 tokens)
+    static constexpr int CHUNKS = 2 * K_CHUNKS;          // K + V tiles, same size
+    static constexpr int BYTES = CHUNKS * 16;
+    static constexpr int KP = (K_CHUNKS + 255) / 256;  // per-thread chunks of each tile
+    static constexpr int PER_THREAD = 2 * KP;          // K chunks first, then V chunks
+    // XOR applied to the chunk index of K row r: the 16 rows read by one 16-lane group land in
+    // distinct bank groups
+    __device__ static constexpr int kx(int r) { return RC >= 16 ? (r & 15) : ((r * RC / 16) & (RC - 1)); }
+    // LDS chunk of V row d, half h (bf16 rows are 2 chunks: rows 8..15 of a 16-row group swap halves)
+    __device__ static constexpr int vpos(int d, int h) { return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ ((d >> 3) & 1)) : h); }
+};
 
-template <int D, int KV, bool QF32, int HG>
-__global__ __launch_bounds__(256, 1) void chunked_prefill_kernel(const PrefillArgs a) {
+template <int D, int KV, bool QF32>
+__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(const PrefillArgs a) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;
@@ -56,12 +71,15 @@ __global__ __launch_bounds__(256, 1) void chunked_prefill_kernel(const PrefillAr
     constexpr int TILE = 16 * D;
     using KR = typename Raw::K;
     using VR = typename Raw::V;
-    __shared__ float s_m[4][HG][16], s_l[4][HG][16];
-    __shared__ float s_x[2][D][16];
+    using TL = PrefillTile<D, ELT>;
+    constexpr int PT = TL::PER_THREAD;
+    constexpr int R = 4;  // blocks in flight (register staging)
+    __shared__ __align__(16) uint4 s_tile[2][TL::CHUNKS];
 
     const int qt = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q4 = lane >> 4, n = lane & 15;
     const int G = a.group, Hkv = a.num_kv_heads, Hq = Hkv * G;
 
@@ -75,27 +93,66 @@ __global__ __launch_bounds__(256, 1) void chunked_prefill_kernel(const PrefillAr
     const bool causal = a.mask_mode == 0 || (a.mask_mode == 1 && P > 0);
     const int kmax = causal ? min(T, P + i0 + nq) : T;  // keys any query of the tile may see
     const int nkb = (kmax + 15) / 16;
-    const int nb = nkb > wave ? (nkb - wave + 3) / 4 : 0;  // this wave's blocks: wave + 4j
-    // this lane's query (column n of S^T) sees keys [0, klim)
     const bool qvalid = n < nq;
-    const int klim = causal ? min(T, P + i0 + n + 1) : T;
+    const int klim = causal ? min(T, P + i0 + n + 1) : T;  // this lane's query sees keys [0, klim)
 
     const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
     const char* kc = static_cast<const char*>(a.k_cache);
     const char* vc = static_cast<const char*>(a.v_cache);
-    const int k_lane_off = (n * D + 8 * q4) * ELT;
-    const int v_lane_off = (n * 16 + 4 * q4) * ELT;
 
-    for (int g0 = 0; g0 < G; g0 += HG) {
-        // Q^T operands: lane (q4, n) holds query i0 + n of head kvh*G + g0 + h, dims 32s + 8q4 .. +8.
-        bf16x8_t qhi[HG][NSLAB], qlo[QF32 ? HG : 1][QF32 ? NSLAB : 1];
+    // This thread's chunks of a block: entry k < KP is a K chunk, the others V chunks (so each
+    // load uses one descriptor for the whole wave); byte offset within the tile (past the end for a
+    // thread without a chunk: such loads return zeros) and LDS chunk.
+    int g_off[PT], l_pos[PT];
+    bool live[PT];
 #pragma unroll
-        for (int h = 0; h < HG; h++) {
-            const int head = kvh * G + g0 + h;
+    for (int k = 0; k < PT; k++) {
+        const int c = tid + 256 * (k % TL::KP);
+        live[k] = c < TL::K_CHUNKS;
+        g_off[k] = live[k] ? c * 16 : TILE * ELT;
+        if (k < TL::KP) {
+            const int r = c / TL::RC, cc = c % TL::RC;
+            l_pos[k] = r * TL::RC + (cc ^ TL::kx(r));
+        } else {
+            l_pos[k] = TL::vpos(c / TL::VRC, c % TL::VRC);
+        }
+    }
+    // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS: reading them there
+    // costs no wait on the streaming loads (a table load inside the stream would).
+    constexpr int KCH = 1024;
+    __shared__ int s_ids[KCH];
+    __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH : 1];
+    // Loads of a block into staging registers through per-block buffer descriptors: an invalid
+    // block or one past the end gets zero-sized descriptors and reads as zeros. The loads are the
+    // same on every step (no branches), so each wait is for exactly the block it needs.
+    auto stage = [&](uint4 (&st)[PT], int jl, int nkc) {
+        const int bid = jl < nkc ? s_ids[jl] : -1;
+        const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
+        const int bytes = bid >= 0 ? TILE * ELT : 0;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+#pragma unroll
+        for (int k = 0; k < PT; k++) st[k] = buffer_load<uint4>(k < TL::KP ? rk : rv, g_off[k]);
+    };
+    auto publish = [&](const uint4 (&st)[PT], int slot) {
+#pragma unroll
+        for (int k = 0; k < PT; k++)
+            if (live[k]) s_tile[slot][l_pos[k]] = st[k];
+    };
+
+    for (int g0 = 0; g0 < G; g0 += 4) {
+        const int g = g0 + wave;
+        const bool active = g < G;  // waves without a head still stage blocks
+        const int head = kvh * G + (active ? g : 0);
+        // Q^T operand: lane (q4, n) holds query i0 + n of this head, dims 32s + 8q4 .. +8.
+        bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
+        {
             const int64_t qrow = (static_cast<int64_t>(q0 + i0 + (qvalid ? n : 0)) * Hq + head) * D;
 #pragma unroll
-            for (int s = 0; s < NSLAB; s++) {
-                const int d0 = 32 * s + 8 * q4;
+            for (int sl = 0; sl < NSLAB; sl++) {
+                const int d0 = 32 * sl + 8 * q4;
                 if constexpr (QF32) {
                     const float* qp = static_cast<const float*>(a.q) + qrow + d0;
                     float x[8];
@@ -109,231 +166,164 @@ __global__ __launch_bounds__(256, 1) void chunked_prefill_kernel(const PrefillAr
                         const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
                         ll[e] = pack_bf16_trunc(r0, r1);
                     }
-                    qhi[h][s] = __builtin_bit_cast(bf16x8_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
-                    qlo[h][s] = __builtin_bit_cast(bf16x8_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+                    qhi[sl] = __builtin_bit_cast(bf16x8_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+                    qlo[sl] = __builtin_bit_cast(bf16x8_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
                 } else {
                     const uint4 raw = qvalid
                         ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
                         : make_uint4(0, 0, 0, 0);
-                    qhi[h][s] = __builtin_bit_cast(bf16x8_t, raw);
+                    qhi[sl] = __builtin_bit_cast(bf16x8_t, raw);
                 }
             }
         }
 
-        // This wave's key blocks go in windows of 64: lane j holds the id (and int8 scales) of
-        // block wave + 4 (w0 + j), loaded once per window, so the streaming loop issues only the
-        // K/V loads (a table load inside it would make the wave wait for every load before it).
-        int my_bid = -1;
-        float my_ks = 0.0f, my_vs = 0.0f;
-        auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j, int nbw) {
-            int bid = j < nbw ? __builtin_amdgcn_readlane(my_bid, j) : -1;
-            bid = bid < a.num_blocks ? bid : -1;
-            const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
-            const int bytes = bid >= 0 ? TILE * ELT : 0;
-            const __amdgpu_buffer_rsrc_t rk =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
-            const __amdgpu_buffer_rsrc_t rv =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+        float m_run = -INFINITY, l_run = 0.0f;
+        f32x4_t acc[NT];
 #pragma unroll
-            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR>(rk, k_lane_off + 32 * s * ELT);
-#pragma unroll
-            for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
-        };
+        for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-        float m_run[HG], l_run[HG];
-        f32x4_t acc[HG][NT];
+        auto compute = [&](int slot, int lb, int jl) {
+            const uint4* tl = s_tile[slot];
+            const char* tb = reinterpret_cast<const char*>(tl);
+            KR kr[NSLAB];
+            VR vr[NT];
 #pragma unroll
-        for (int h = 0; h < HG; h++) {
-            m_run[h] = -INFINITY;
-            l_run[h] = 0.0f;
+            for (int sl = 0; sl < NSLAB; sl++) {
+                if constexpr (ELT == 2) {  // 8 bf16 = one 16-byte chunk
+                    const int cc = 4 * sl + q4;
+                    kr[sl] = tl[n * TL::RC + (cc ^ TL::kx(n))];
+                } else {  // 8 int8 codes = half a chunk
+                    const int cc = 2 * sl + (q4 >> 1);
+                    kr[sl] = *reinterpret_cast<const KR*>(tb + (n * TL::RC + (cc ^ TL::kx(n))) * 16 + (q4 & 1) * 8);
+                }
+            }
 #pragma unroll
-            for (int t = 0; t < NT; t++) acc[h][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-
-        auto compute = [&](const KR (&kr)[NSLAB], const VR (&vr)[NT], int j, int lb) {
+            for (int t = 0; t < NT; t++) {
+                const int d = 16 * t + n;
+                if constexpr (ELT == 2)
+                    vr[t] = *reinterpret_cast<const VR*>(tb + TL::vpos(d, q4 >> 1) * 16 + (q4 & 1) * 8);
+                else
+                    vr[t] = *reinterpret_cast<const VR*>(tb + TL::vpos(d, 0) * 16 + q4 * 4);
+            }
             float ks = 1.0f, vfac = 1.0f;
-            if constexpr (KV == PA_DTYPE_INT8) {  // an invalid block's tile reads as zeros, scale 0
-                const int bid = __builtin_amdgcn_readlane(my_bid, j);
-                const bool ok = bid >= 0 && bid < a.num_blocks;
-                ks = ok ? readlane_f(my_ks, j) : 0.0f;
-                vfac = ok ? readlane_f(my_vs, j) : 0.0f;
+            if constexpr (KV == PA_DTYPE_INT8) {  // 0 for an invalid block (its tile reads as zeros)
+                ks = s_ksc[jl];
+                vfac = s_vsc[jl];
             }
-            bf16x8_t kop[NSLAB];
+            f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int sl = 0; sl < NSLAB; sl++) kop[sl] = k_operand(kr[sl]);
-            s16x4_t vop[NT];
-#pragma unroll
-            for (int t = 0; t < NT; t++) vop[t] = v_operand(vr[t]);
+            for (int sl = 0; sl < NSLAB; sl++) {
+                const bf16x8_t kop = k_operand(kr[sl]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
+                if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+            }
             const int kbase = lb * 16 + 4 * q4;
-#pragma unroll
-            for (int h = 0; h < HG; h++) {
-                f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int sl = 0; sl < NSLAB; sl++) {
-                    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qhi[h][sl], s, 0, 0, 0);
-                    if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qlo[h][sl], s, 0, 0, 0);
-                }
-                float sc[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float v = s[i];
-                    if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
-                    v = v * a.scale;
-                    // queries past the tile keep finite scores (their rows are never stored)
-                    sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
-                }
-                const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-                const bool grow = bm > m_run[h] + kPrefillRescaleThreshold;
-                if (__any(grow)) {
-                    const float m_new = grow ? bm : m_run[h];
-                    // 0 from -inf; 1 for a query whose max stays -inf (nothing accumulated yet)
-                    const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run[h] - m_new);
-                    l_run[h] *= alpha;
-                    m_run[h] = m_new;
-                    float ar[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
-#pragma unroll
-                    for (int t = 0; t < NT; t++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[h][t][i] *= ar[i];
-                }
-                // A wave sees only every 4th block: all of them may be masked for a query, whose
-                // max then stays -inf; its probabilities are 0, not exp(-inf + inf).
-                float p[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    p[i] = sc[i] == -INFINITY ? 0.0f : __expf(sc[i] - m_run[h]);
-                    l_run[h] += p[i];
-                    if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
-                }
-                uint32_t hi[2], lo[2];
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    const float a0 = p[2 * e], a1 = p[2 * e + 1];
-                    const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
-                    const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
-                    hi[e] = pack_bf16_trunc(a0, a1);
-                    lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
-                }
-                const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
-                const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    acc[h][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop[t], acc[h][t], 0, 0, 0);
-                    acc[h][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop[t], acc[h][t], 0, 0, 0);
-                }
-            }
-        };
-
-        for (int w0 = 0; w0 < nb; w0 += 64) {
-            const int nbw = min(64, nb - w0);
-            my_bid = lane < nbw ? table[wave + 4 * (w0 + lane)] : -1;
-            if constexpr (KV == PA_DTYPE_INT8) {  // unconditional loads (index clamped)
-                const int sb = my_bid >= 0 && my_bid < a.num_blocks ? my_bid : 0;
-                my_ks = a.k_scale[static_cast<int64_t>(sb) * Hkv + kvh];
-                my_vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + kvh];
-            }
-            KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
-            VR va[NT], vb[NT], vx[NT];
-            int j = 0;
-            load(ka, va, 0, nbw);
-            load(kb, vb, 1, nbw);
-            while (j < nbw) {
-                load(kx, vx, j + 2, nbw);
-                compute(ka, va, j, wave + 4 * (w0 + j));
-                if (++j >= nbw) break;
-                load(ka, va, j + 2, nbw);
-                compute(kb, vb, j, wave + 4 * (w0 + j));
-                if (++j >= nbw) break;
-                load(kb, vb, j + 2, nbw);
-                compute(kx, vx, j, wave + 4 * (w0 + j));
-                ++j;
-            }
-        }
-
-        // ---- combine the 4 waves per head: weights exp(m_w - M), then a 2-level tree in LDS ----
-#pragma unroll
-        for (int h = 0; h < HG; h++) {
-            const float l_tot = rows_sum(l_run[h]);
-            if (q4 == 0) {
-                s_m[wave][h][n] = m_run[h];
-                s_l[wave][h][n] = l_tot;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < HG; h++) {
-            float M[4], f_own[4];
+            float sc[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int r = 4 * q4 + i;
-                M[i] = fmaxf(fmaxf(s_m[0][h][r], s_m[1][h][r]), fmaxf(s_m[2][h][r], s_m[3][h][r]));
-                // 0 for a wave that saw no unmasked key of query r (or no block at all)
-                f_own[i] = s_m[wave][h][r] == -INFINITY ? 0.0f : __expf(s_m[wave][h][r] - M[i]);
+                float v = s[i];
+                if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
+                v = v * a.scale;
+                // queries past the tile keep finite scores (their rows are never stored)
+                sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
             }
+            const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+            const bool grow = bm > m_run + kPrefillRescaleThreshold;
+            if (__any(grow)) {
+                const float m_new = grow ? bm : m_run;
+                const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run - m_new);
+                l_run *= alpha;
+                m_run = m_new;
+                float ar[4];
 #pragma unroll
-            for (int t = 0; t < NT; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[h][t][i] *= f_own[i];
-            if (wave >= 2) {
+                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
 #pragma unroll
                 for (int t = 0; t < NT; t++)
-                    *reinterpret_cast<f32x4_t*>(&s_x[wave - 2][16 * t + n][4 * q4]) = acc[h][t];
-            }
-            __syncthreads();
-            if (wave < 2) {
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    f32x4_t* slot = reinterpret_cast<f32x4_t*>(&s_x[wave][16 * t + n][4 * q4]);
-                    acc[h][t] += *slot;
-                    if (wave == 1) *slot = acc[h][t];
+                    for (int i = 0; i < 4; i++) acc[t][i] *= ar[i];
+            }
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = sc[i] == -INFINITY ? 0.0f : __expf(sc[i] - m_run);
+                l_run += p[i];
+                if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
+            }
+            uint32_t hi[2], lo[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float a0 = p[2 * e], a1 = p[2 * e + 1];
+                const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+                const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+                hi[e] = pack_bf16_trunc(a0, a1);
+                lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+            }
+            const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+            const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const s16x4_t vop = v_operand(vr[t]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+            }
+        };
+
+        // Stream: block j is published into slot j % 2 at step j (its staging registers were
+        // loaded R steps earlier), the registers are refilled with block j + R, one barrier, then
+        // every wave computes block j. Slot j % 2 was last read by compute(j - 2), which every
+        // wave finished before the barrier of step j - 1. Whole rounds of R steps keep the
+        // staging registers' indices static.
+        for (int c0 = 0; c0 < nkb; c0 += KCH) {
+            const int nkc = min(KCH, nkb - c0);
+            __syncthreads();  // the previous chunk's ids and the slots are no longer read
+            for (int i = tid; i < nkc; i += 256) {
+                int id = table[c0 + i];
+                id = id < a.num_blocks ? id : -1;
+                s_ids[i] = id;
+                if constexpr (KV == PA_DTYPE_INT8) {
+                    s_ksc[i] = id >= 0 ? a.k_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
+                    s_vsc[i] = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
                 }
             }
             __syncthreads();
-            if (wave == 0) {
-                float L[4];
+            uint4 stg[R][PT];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = 4 * q4 + i;
-                    L[i] = 0.0f;
+            for (int r = 0; r < R; r++) stage(stg[r], r, nkc);
+            for (int j0 = 0; j0 < nkc; j0 += R) {
 #pragma unroll
-                    for (int w = 0; w < 4; w++)
-                        L[i] += s_m[w][h][r] == -INFINITY ? 0.0f : s_l[w][h][r] * __expf(s_m[w][h][r] - M[i]);
-                }
-                const int head = kvh * G + g0 + h;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int qi = 4 * q4 + i;
-                    if (qi < nq) {
-                        const float inv = 1.0f / L[i];
-                        float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
-#pragma unroll
-                        for (int t = 0; t < NT; t++) {
-                            const f32x4_t other = *reinterpret_cast<const f32x4_t*>(&s_x[1][16 * t + n][4 * q4]);
-                            o[16 * t + n] = (acc[h][t][i] + other[i]) * inv;
-                        }
-                    }
+                for (int r = 0; r < R; r++) {
+                    // the last round's steps past the end publish and stage zeros: harmless, and
+                    // the loads stay the same on every step
+                    const int jl = j0 + r;
+                    publish(stg[r], jl & 1);
+                    stage(stg[r], jl + R, nkc);
+                    __syncthreads();
+                    if (active && jl < nkc) compute(jl & 1, c0 + jl, jl);
                 }
             }
-            __syncthreads();  // s_x reuse by the next head
+        }
+        __syncthreads();  // the slots are reused by the next head group
+
+        // rows of acc are queries 4q4 + i; their sums live in lanes (any q4, n = 4q4 + i)
+        const float l_tot = rows_sum(l_run);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qi = 4 * q4 + i;
+            const float li = __shfl(l_tot, qi, 64);
+            if (active && qi < nq) {
+                const float inv = 1.0f / li;
+                float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
+#pragma unroll
+                for (int t = 0; t < NT; t++) o[16 * t + n] = acc[t][i] * inv;
+            }
         }
     }
 }
 
 template <int D, int KV>
 void launch(const PrefillArgs& a, bool qf32, dim3 grid, hipStream_t s) {
-    // the heads per pass must divide the group; other group sizes run one head per pass
-    if (qf32) {
-        constexpr int HG = prefill_heads_per_pass<D, true>();
-        if (a.group % HG == 0) chunked_prefill_kernel<D, KV, true, HG><<<grid, 256, 0, s>>>(a);
-        else chunked_prefill_kernel<D, KV, true, 1><<<grid, 256, 0, s>>>(a);
-    } else {
-        constexpr int HG = prefill_heads_per_pass<D, false>();
-        if (a.group % HG == 0) chunked_prefill_kernel<D, KV, false, HG><<<grid, 256, 0, s>>>(a);
-        else if (HG > 2 && a.group % 2 == 0) chunked_prefill_kernel<D, KV, false, (HG > 2 ? 2 : 1)><<<grid, 256, 0, s>>>(a);
-        else chunked_prefill_kernel<D, KV, false, 1><<<grid, 256, 0, s>>>(a);
-    }
+    if (qf32) chunked_prefill_kernel<D, KV, true><<<grid, 256, 0, s>>>(a);
+    else chunked_prefill_kernel<D, KV, false><<<grid, 256, 0, s>>>(a);
 }
 
 template <int D>
