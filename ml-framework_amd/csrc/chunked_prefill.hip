@@ -8,17 +8,21 @@
 // (ContinuousBatching/Prefill/PrefillHandler.cs:85-89, PrefillConfiguration.cs:21); each chunk is
 // one call here.
 //
-// Work decomposition: one workgroup per (16-query tile, KV head, sequence); wave w computes query
-// head w (w + 4, ...) of the KV head's group. The workgroup streams the key blocks through LDS:
-// each thread loads its 16-byte pieces of a block's K and V tiles into registers R blocks ahead,
-// writes them into one of two LDS slots, and after one barrier every wave reads its MFMA operands
-// from that slot. A K/V tile thus crosses from memory once per workgroup and R blocks are in
-// flight per workgroup. The LDS tiles are stored with an XOR swizzle of 16-byte chunks so the
-// operand reads are free of bank conflicts. Per 16-key block and head:
-// S^T[16 keys][16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16, online softmax per query in fp32
-// with the causal limit per query, O[16 queries][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
-// split into bf16 high and low parts. These are the decode kernel's operand layouts with the 16
-// MFMA rows holding 16 queries instead of (padded) heads.
+// Work decomposition: the units are (16-query tile, query head) pairs of one KV head. A
+// workgroup of 4 waves takes 2 (G = 4) or more consecutive query tiles of one (sequence, KV head)
+// -- all of them on one XCD, the heaviest first -- and each wave computes two units on the same
+// K/V operands. The workgroup streams the key blocks through LDS two at a time: each thread
+// loads its 16-byte pieces of the pair's K and V tiles into registers one step ahead, writes
+// them into one of two LDS slots, and after one barrier every wave reads its MFMA operands from
+// that slot, so a K/V tile crosses from memory once per workgroup. The LDS tiles are stored with
+// an XOR swizzle of 16-byte chunks (and the pair's second tile offset by half a bank line) so the
+// operand reads are free of bank conflicts. Per pair of blocks and unit:
+// S^T[32 keys][16 queries] = K . Q^T on two v_mfma_f32_16x16x32_bf16 per 32 dims, whose rows are
+// permuted so every lane ends up with 8 consecutive keys of one block; online softmax per query
+// in fp32 (log2 domain, rescale only past a 2^12 margin, mask only on the pairs at the causal
+// edge); O[16 queries][D] += P . V on v_mfma_f32_16x16x32_bf16 with P split into bf16 high and
+// low parts and the lane's 8 keys as the k range, the V operand one 16-byte LDS read; the row
+// sums of P from the same MFMA against ones.
 #include <string>
 
 #include "decode_common.h"
@@ -42,9 +46,19 @@ struct PrefillArgs {
     int32_t num_blocks;
     int32_t mask_mode;  // 0 causal, 1 causal only when the prefix is non-empty, 2 no mask
     float scale;
+    int32_t qtiles_per_wg;  // 16-query tiles per workgroup: max(1, kPrefillUnits / group)
+    int32_t num_qgroups;    // workgroups per (sequence, KV head): tiles of the longest chunk / QT
+    int32_t num_groups;     // num_seqs * num_kv_heads
 };
 
-constexpr float kPrefillRescaleThreshold = 8.0f;
+// The running maximum (log2 units) is raised only when a block's maximum exceeds it by more than
+// this, so unnormalised probabilities stay below 2^12 and the rescale of the accumulators is rare.
+constexpr float kPrefillRescaleLog2 = 12.0f;
+
+// Waves per workgroup; each computes two (query tile, query head) units.
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
+constexpr int kPrefillUnits = 2 * kPrefillWaves;  // units per workgroup round
 
 // LDS geometry of one staged block (K tile then V tile) for head_dim D and element size ELT.
 template <int D, int ELT> struct PrefillTile {
@@ -53,48 +67,75 @@ template <int D, int ELT> struct PrefillTile {
     static constexpr int VRC = ELT;                      // 16-byte chunks per V row (16 tokens)
     static constexpr int CHUNKS = 2 * K_CHUNKS;          // K + V tiles, same size
     static constexpr int BYTES = CHUNKS * 16;
-    static constexpr int KP = (K_CHUNKS + 255) / 256;  // per-thread chunks of each tile
+    static constexpr int KP = (K_CHUNKS + kPrefillThreads - 1) / kPrefillThreads;  // per-thread chunks of each tile
     static constexpr int PER_THREAD = 2 * KP;          // K chunks first, then V chunks
-    // XOR applied to the chunk index of K row r: the 16 rows read by one 16-lane group land in
-    // distinct bank groups
-    __device__ static constexpr int kx(int r) { return RC >= 16 ? (r & 15) : ((r * RC / 16) & (RC - 1)); }
-    // LDS chunk of V row d, half h (bf16 rows are 2 chunks: rows 8..15 of a 16-row group swap halves)
-    __device__ static constexpr int vpos(int d, int h) { return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ ((d >> 3) & 1)) : h); }
+    // K row r's chunk c is stored at chunk r * RC + (c ^ kx(r)). One QK operand read (8 lanes)
+    // takes one chunk column of 4 consecutive rows in each of the pair's two tiles, whose bases
+    // differ by half a 128-byte bank line: kx spreads the 4 rows over the other 2 bits of the
+    // line's 8 chunk positions. It only touches the chunk index's low 2 bits (the lane group's
+    // part), so the slab part stays an immediate offset.
+    __device__ static constexpr int kx(int r) { return r & 3; }
+    // Chunk offset of block b of slot `slot` in the LDS ring: block 1 sits 4 chunks (64 bytes)
+    // further, so equal positions in the two tiles fall in opposite halves of a bank line.
+    static constexpr int SLOT = 2 * CHUNKS + 8;
+    __device__ static constexpr int base(int slot, int b) { return slot * SLOT + b * (CHUNKS + 4); }
+    // LDS chunk of V row d, half h. A PV operand read takes one half of 8 consecutive rows; bf16
+    // rows are 2 chunks, and rows 4..7 of each 8 swap halves so the 8 reads hit 8 distinct positions.
+    __device__ static constexpr int vpos(int d, int h) { return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ ((d >> 2) & 1)) : h); }
+
 };
 
+// Work units are (16-query tile, query head) pairs of one KV head. A workgroup takes QT =
+// max(1, kPrefillUnits / G) consecutive query tiles, i.e. QT * G units, kPrefillUnits at a time:
+// wave w computes units 2w and 2w + 1 of the round on the same K/V operands (each LDS operand
+// read feeds both).
 template <int D, int KV, bool QF32>
-__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) void chunked_prefill_kernel(const PrefillArgs a) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;
     constexpr int NT = D / 16;
     constexpr int TILE = 16 * D;
     using KR = typename Raw::K;
-    using VR = typename Raw::V;
     using TL = PrefillTile<D, ELT>;
     constexpr int PT = TL::PER_THREAD;
-    constexpr int R = 4;  // blocks in flight (register staging)
-    __shared__ __align__(16) uint4 s_tile[2][TL::CHUNKS];
+    constexpr int R = 1;  // block pairs in flight (register staging): 1 or 2
+    __shared__ __align__(16) uint4 s_tile[2 * TL::SLOT];  // 2 slots x 2 blocks (TL::base)
 
-    const int qt = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    // Workgroup -> (query-tile group, KV head, sequence). Workgroup ids are dispatched to the 8
+    // XCDs in turn (id mod 8); every query-tile group of (sequence, KV head) group gi runs on XCD
+    // gi mod 8, so the workgroups that read the same K/V blocks share one L2, and within a group
+    // the ones with the most keys (the last ones) start first.
+    const int lid = blockIdx.x;
+    const int wk = lid >> 3;
+    const int m = wk / a.num_qgroups;
+    const int qg = a.num_qgroups - 1 - (wk - m * a.num_qgroups);
+    const int gi = (lid & 7) + 8 * m;
+    if (gi >= a.num_groups) return;
+    const int seq = gi / a.num_kv_heads, kvh = gi - seq * a.num_kv_heads;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q4 = lane >> 4, n = lane & 15;
     const int G = a.group, Hkv = a.num_kv_heads, Hq = Hkv * G;
+    const int QT = a.qtiles_per_wg;
 
     const int q0 = a.q_start_loc[seq];
     const int Lc = a.q_start_loc[seq + 1] - q0;
     const int P = max(a.prefix_lens[seq], 0);
-    const int i0 = qt * 16;
-    if (i0 >= Lc) return;
-    const int nq = min(16, Lc - i0);
+    const int i0w = qg * QT * 16;  // the workgroup's queries are [i0w, iew) of the chunk
+    if (i0w >= Lc) return;
+    const int iew = min(Lc, i0w + QT * 16);
     const int T = min(P + Lc, a.max_blocks_per_seq * 16);
     const bool causal = a.mask_mode == 0 || (a.mask_mode == 1 && P > 0);
-    const int kmax = causal ? min(T, P + i0 + nq) : T;  // keys any query of the tile may see
+    const int kmax = causal ? min(T, P + iew) : T;  // keys any query of the workgroup may see
     const int nkb = (kmax + 15) / 16;
-    const bool qvalid = n < nq;
-    const int klim = causal ? min(T, P + i0 + n + 1) : T;  // this lane's query sees keys [0, klim)
+    const int klim_lo = causal ? min(T, P + i0w + 1) : T;  // every query of it sees [0, klim_lo)
+    const float c2 = a.scale * 1.4426950408889634f;       // scores in log2 units
+    // QK operand row of this lane (see compute) and the keys it holds after QK (for P and V)
+    const int krow0 = (n & 3) + 8 * (n >> 3), kblk = (n >> 2) & 1;
+    const int pblk = q4 & 1, ptok = 8 * (q4 >> 1);
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
 
     const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
     const char* kc = static_cast<const char*>(a.k_cache);
@@ -107,7 +148,7 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
     bool live[PT];
 #pragma unroll
     for (int k = 0; k < PT; k++) {
-        const int c = tid + 256 * (k % TL::KP);
+        const int c = tid + kPrefillThreads * (k % TL::KP);
         live[k] = c < TL::K_CHUNKS;
         g_off[k] = live[k] ? c * 16 : TILE * ELT;
         if (k < TL::KP) {
@@ -121,35 +162,55 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
     // costs no wait on the streaming loads (a table load inside the stream would).
     constexpr int KCH = 1024;
     __shared__ int s_ids[KCH];
-    __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH : 1];
+    __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1];
     // Loads of a block into staging registers through per-block buffer descriptors: an invalid
     // block or one past the end gets zero-sized descriptors and reads as zeros. The loads are the
     // same on every step (no branches), so each wait is for exactly the block it needs.
-    auto stage = [&](uint4 (&st)[PT], int jl, int nkc) {
-        const int bid = jl < nkc ? s_ids[jl] : -1;
-        const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
-        const int bytes = bid >= 0 ? TILE * ELT : 0;
-        const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+    auto stage = [&](uint4 (&st)[2][PT], int jl, int nkc) {  // blocks jl, jl + 1
 #pragma unroll
-        for (int k = 0; k < PT; k++) st[k] = buffer_load<uint4>(k < TL::KP ? rk : rv, g_off[k]);
+        for (int b = 0; b < 2; b++) {
+            const int bid = jl + b < nkc ? s_ids[jl + b] : -1;
+            const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
+            const int bytes = bid >= 0 ? TILE * ELT : 0;
+            const __amdgpu_buffer_rsrc_t rk =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t rv =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+#pragma unroll
+            for (int k = 0; k < PT; k++) st[b][k] = buffer_load<uint4>(k < TL::KP ? rk : rv, g_off[k]);
+        }
     };
-    auto publish = [&](const uint4 (&st)[PT], int slot) {
+    auto publish = [&](const uint4 (&st)[2][PT], int slot) {
 #pragma unroll
-        for (int k = 0; k < PT; k++)
-            if (live[k]) s_tile[slot][l_pos[k]] = st[k];
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int k = 0; k < PT; k++)
+                if (live[k]) s_tile[TL::base(slot, b) + l_pos[k]] = st[b][k];
     };
 
-    for (int g0 = 0; g0 < G; g0 += 4) {
-        const int g = g0 + wave;
-        const bool active = g < G;  // waves without a head still stage blocks
-        const int head = kvh * G + (active ? g : 0);
-        // Q^T operand: lane (q4, n) holds query i0 + n of this head, dims 32s + 8q4 .. +8.
-        bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
-        {
-            const int64_t qrow = (static_cast<int64_t>(q0 + i0 + (qvalid ? n : 0)) * Hq + head) * D;
+    const int U = QT * G;
+    for (int u0 = 0; u0 < U; u0 += kPrefillUnits) {
+        // This wave's two units. A unit past U repeats unit u0 and a query tile past the chunk has
+        // no valid query: both are computed like the others (no branch) and never stored.
+        int head[2], i0[2], nq[2], klim[2];
+        bool store[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int u = u0 + 2 * wave + k;
+            const int uu = u < U ? u : u0;
+            const int qtl = uu / G;
+            head[k] = kvh * G + (uu - qtl * G);
+            i0[k] = i0w + 16 * qtl;
+            nq[k] = max(0, min(16, Lc - i0[k]));
+            store[k] = u < U && nq[k] > 0;
+            klim[k] = causal ? min(T, P + i0[k] + n + 1) : T;  // query n sees keys [0, klim)
+        }
+        // Q^T operands: lane (q4, n) holds query i0 + n of the unit's head, dims 32s + 8q4 .. +8.
+        bf16x8_t qhi[2][NSLAB], qlo[2][QF32 ? NSLAB : 1];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const bool qvalid = n < nq[k];
+            const int64_t qrow = (static_cast<int64_t>(q0 + i0[k] + (qvalid ? n : 0)) * Hq + head[k]) * D;
 #pragma unroll
             for (int sl = 0; sl < NSLAB; sl++) {
                 const int d0 = 32 * sl + 8 * q4;
@@ -166,117 +227,171 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
                         const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
                         ll[e] = pack_bf16_trunc(r0, r1);
                     }
-                    qhi[sl] = __builtin_bit_cast(bf16x8_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
-                    qlo[sl] = __builtin_bit_cast(bf16x8_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+                    qhi[k][sl] = __builtin_bit_cast(bf16x8_t, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+                    qlo[k][sl] = __builtin_bit_cast(bf16x8_t, make_uint4(ll[0], ll[1], ll[2], ll[3]));
                 } else {
                     const uint4 raw = qvalid
                         ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
                         : make_uint4(0, 0, 0, 0);
-                    qhi[sl] = __builtin_bit_cast(bf16x8_t, raw);
+                    qhi[k][sl] = __builtin_bit_cast(bf16x8_t, raw);
                 }
             }
         }
 
-        float m_run = -INFINITY, l_run = 0.0f;
-        f32x4_t acc[NT];
+        float m_run[2] = {-INFINITY, -INFINITY};  // log2 units, query n
+        float l_run[2] = {0.0f, 0.0f};            // int8: sum of P for query n over this lane's keys
+        f32x4_t acc_l[2], acc[2][NT];             // bf16: row sums of P; outputs (queries 4q4 + i)
 #pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < 2; k++) {
+            acc_l[k] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[k][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 
-        auto compute = [&](int slot, int lb, int jl) {
-            const uint4* tl = s_tile[slot];
-            const char* tb = reinterpret_cast<const char*>(tl);
-            KR kr[NSLAB];
-            VR vr[NT];
+        // One pair of blocks (keys lb*16 .. lb*16 + 31), lanes (q4, n): the two QK MFMAs h = 0, 1 take
+        // as row r key 8 (r >> 3) + 4h + (r & 3) of block (r >> 2) & 1, so lane (q4, n) receives, for
+        // query n, scores e = 4h + i of keys ptok + e of block pblk: 8 consecutive keys of one block.
+        // That is exactly the k range the lane feeds the PV MFMA (v_mfma_f32_16x16x32_bf16, k = 8q4 +
+        // e), in P and in V, where the V operand is then one 16-byte LDS read. Row sums come from a
+        // third MFMA against ones, in the accumulators' own layout. Scores are kept in log2 units
+        // (scale * log2(e) folded in); pairs with every key below every query's causal limit skip
+        // the mask. Both units use the same K and V operands.
+        auto compute = [&](bool masked, int kend, int slot, int lb, int jl) {
+            const char* tk = reinterpret_cast<const char*>(s_tile + TL::base(slot, kblk));
+            const char* tv = reinterpret_cast<const char*>(s_tile + TL::base(slot, pblk));
+            // QK per half h (its 16-row K operands are then dead), V operands after QK
+            float v[2][8];
 #pragma unroll
-            for (int sl = 0; sl < NSLAB; sl++) {
-                if constexpr (ELT == 2) {  // 8 bf16 = one 16-byte chunk
-                    const int cc = 4 * sl + q4;
-                    kr[sl] = tl[n * TL::RC + (cc ^ TL::kx(n))];
-                } else {  // 8 int8 codes = half a chunk
-                    const int cc = 2 * sl + (q4 >> 1);
-                    kr[sl] = *reinterpret_cast<const KR*>(tb + (n * TL::RC + (cc ^ TL::kx(n))) * 16 + (q4 & 1) * 8);
+            for (int h = 0; h < 2; h++) {
+                const int r = krow0 + 4 * h;
+                bf16x8_t kop[NSLAB];
+#pragma unroll
+                for (int sl = 0; sl < NSLAB; sl++) {
+                    if constexpr (ELT == 2) {  // 8 bf16 = one 16-byte chunk
+                        const int cc = 4 * sl + q4;
+                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + (r * TL::RC + (cc ^ TL::kx(r))) * 16));
+                    } else {  // 8 int8 codes = half a chunk
+                        const int cc = 2 * sl + (q4 >> 1);
+                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + (r * TL::RC + (cc ^ TL::kx(r))) * 16 + (q4 & 1) * 8));
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int sl = 0; sl < NSLAB; sl++) {
+                        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qhi[k][sl], sacc, 0, 0, 0);
+                        if constexpr (QF32) sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[sl], qlo[k][sl], sacc, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[k][4 * h + i] = sacc[i];
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep the V reads after QK (register pressure)
+            bf16x8_t vop[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const int d = 16 * t + n;
-                if constexpr (ELT == 2)
-                    vr[t] = *reinterpret_cast<const VR*>(tb + TL::vpos(d, q4 >> 1) * 16 + (q4 & 1) * 8);
-                else
-                    vr[t] = *reinterpret_cast<const VR*>(tb + TL::vpos(d, 0) * 16 + q4 * 4);
+                if constexpr (ELT == 2) vop[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1) * 16));
+                else vop[t] = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0) * 16 + (q4 >> 1) * 8));
             }
-            float ks = 1.0f, vfac = 1.0f;
-            if constexpr (KV == PA_DTYPE_INT8) {  // 0 for an invalid block (its tile reads as zeros)
-                ks = s_ksc[jl];
-                vfac = s_vsc[jl];
+            if constexpr (KV == PA_DTYPE_INT8) {
+                const float mult = c2 * s_ksc[jl + pblk];  // 0 for an invalid block
+#pragma unroll
+                for (int k = 0; k < 2; k++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[k][e] *= mult;
             }
-            f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (masked) {  // wave-uniform; only the pairs at the causal edge or past the end
+                const int kq = (lb + pblk) * 16 + ptok;
 #pragma unroll
-            for (int sl = 0; sl < NSLAB; sl++) {
-                const bf16x8_t kop = k_operand(kr[sl]);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
-                if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+                for (int k = 0; k < 2; k++) {
+                    const int lim = min(klim[k], kend) - kq;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[k][e] = e < lim ? v[k][e] : -INFINITY;
+                }
             }
-            const int kbase = lb * 16 + 4 * q4;
-            float sc[4];
+            float bm[2];
+            bool grow[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float v = s[i];
-                if constexpr (KV == PA_DTYPE_INT8) v = v * ks;
-                v = v * a.scale;
-                // queries past the tile keep finite scores (their rows are never stored)
-                sc[i] = !qvalid ? 0.0f : (kbase + i < klim ? v : -INFINITY);
+            for (int k = 0; k < 2; k++) {
+                const float bl = fmaxf(fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])),
+                                       fmaxf(fmaxf(v[k][4], v[k][5]), fmaxf(v[k][6], v[k][7])));
+                bm[k] = rows_max(bl);
+                if constexpr (KV != PA_DTYPE_INT8) bm[k] *= c2;
+                grow[k] = bm[k] > m_run[k] + kPrefillRescaleLog2;
             }
-            const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            const bool grow = bm > m_run + kPrefillRescaleThreshold;
-            if (__any(grow)) {
-                const float m_new = grow ? bm : m_run;
-                const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run - m_new);
-                l_run *= alpha;
-                m_run = m_new;
-                float ar[4];
+            if (__any(grow[0] || grow[1])) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
+                for (int k = 0; k < 2; k++) {
+                    const float m_new = grow[k] ? bm[k] : m_run[k];
+                    const float alpha = __builtin_amdgcn_exp2f(m_run[k] - m_new);  // 0 on the first update
+                    m_run[k] = m_new;
+                    l_run[k] *= alpha;
+                    float ar[4];
 #pragma unroll
-                for (int t = 0; t < NT; t++)
+                    for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * q4 + i, 64);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[t][i] *= ar[i];
+                    for (int i = 0; i < 4; i++) acc_l[k][i] *= ar[i];
+#pragma unroll
+                    for (int t = 0; t < NT; t++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[k][t][i] *= ar[i];
+                }
             }
-            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                p[i] = sc[i] == -INFINITY ? 0.0f : __expf(sc[i] - m_run);
-                l_run += p[i];
-                if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
-            }
-            uint32_t hi[2], lo[2];
+            for (int k = 0; k < 2; k++) {
+                float p[8];
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const float a0 = p[2 * e], a1 = p[2 * e + 1];
-                const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
-                const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
-                hi[e] = pack_bf16_trunc(a0, a1);
-                lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
-            }
-            const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
-            const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+                for (int e = 0; e < 8; e++) {
+                    if constexpr (KV == PA_DTYPE_INT8) p[e] = __builtin_amdgcn_exp2f(v[k][e] - m_run[k]);
+                    else p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[k][e], c2, -m_run[k]));
+                }
+                if constexpr (KV == PA_DTYPE_INT8) {  // the row sums take P before the block's V scale
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const s16x4_t vop = v_operand(vr[t]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+                    for (int e = 0; e < 8; e++) l_run[k] += p[e];
+                    const float vs = s_vsc[jl + pblk];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) p[e] *= vs;
+                }
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float a0 = p[2 * e], a1 = p[2 * e + 1];
+                    const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+                    const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+                    hi[e] = pack_bf16_trunc(a0, a1);
+                    lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+                }
+                const bf16x8_t phi = __builtin_bit_cast(bf16x8_t, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                const bf16x8_t plo = __builtin_bit_cast(bf16x8_t, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop[t], acc[k][t], 0, 0, 0);
+                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop[t], acc[k][t], 0, 0, 0);
+                }
+                if constexpr (KV != PA_DTYPE_INT8) {
+                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, ones, acc_l[k], 0, 0, 0);
+                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, ones, acc_l[k], 0, 0, 0);
+                }
             }
         };
 
-        // Stream: block j is published into slot j % 2 at step j (its staging registers were
-        // loaded R steps earlier), the registers are refilled with block j + R, one barrier, then
-        // every wave computes block j. Slot j % 2 was last read by compute(j - 2), which every
-        // wave finished before the barrier of step j - 1. Whole rounds of R steps keep the
-        // staging registers' indices static.
+        // Stream, a pair of blocks per step: pair j (blocks 2j, 2j + 1 of the chunk) is published
+        // into slot j % 2 at step j (its staging registers were loaded R steps earlier), the
+        // registers are refilled with pair j + R, one barrier, then every wave computes pair j.
+        // Slot j % 2 was last read by compute(j - 2), which every wave finished before the
+        // barrier of step j - 1. Whole rounds of 2 steps keep the slot and the staging registers'
+        // indices static; a step past the end publishes and stages zeros and computes with every
+        // key masked (harmless, and the loads and the compute stay the same on every step: a
+        // branch around the compute would make the accumulators change registers).
         for (int c0 = 0; c0 < nkb; c0 += KCH) {
             const int nkc = min(KCH, nkb - c0);
+            const int npair = (nkc + 1) / 2;
+            const int kend = (c0 + nkc) * 16;        // keys of this chunk of the table end here
+            const int kend_lo = min(klim_lo, kend);  // pairs reaching past it need the mask
             __syncthreads();  // the previous chunk's ids and the slots are no longer read
-            for (int i = tid; i < nkc; i += 256) {
+            for (int i = tid; i < nkc; i += kPrefillThreads) {
                 int id = table[c0 + i];
                 id = id < a.num_blocks ? id : -1;
                 s_ids[i] = id;
@@ -285,36 +400,51 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
                     s_vsc[i] = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
                 }
             }
+            if constexpr (KV == PA_DTYPE_INT8) {  // blocks past the end (an odd chunk's partner, a step
+                if (tid < 4) {                      // past the end): scale 0
+                    s_ksc[nkc + tid] = 0.0f;
+                    s_vsc[nkc + tid] = 0.0f;
+                }
+            }
             __syncthreads();
-            uint4 stg[R][PT];
+            uint4 stg[R][2][PT];
 #pragma unroll
-            for (int r = 0; r < R; r++) stage(stg[r], r, nkc);
-            for (int j0 = 0; j0 < nkc; j0 += R) {
+            for (int r = 0; r < R; r++) stage(stg[r], 2 * r, nkc);
+            for (int j0 = 0; j0 < npair; j0 += 2) {
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    // the last round's steps past the end publish and stage zeros: harmless, and
-                    // the loads stay the same on every step
-                    const int jl = j0 + r;
-                    publish(stg[r], jl & 1);
-                    stage(stg[r], jl + R, nkc);
+                for (int u = 0; u < 2; u++) {  // u = the slot, so LDS offsets are static
+                    const int jp = j0 + u;
+                    publish(stg[u % R], u);
+                    stage(stg[u % R], 2 * (jp + R), nkc);
                     __syncthreads();
-                    if (active && jl < nkc) compute(jl & 1, c0 + jl, jl);
+                    const int lb = c0 + 2 * jp;
+                    compute((lb + 2) * 16 > kend_lo, kend, u, lb, 2 * jp);
                 }
             }
         }
-        __syncthreads();  // the slots are reused by the next head group
+        __syncthreads();  // the slots are reused by the next round
 
-        // rows of acc are queries 4q4 + i; their sums live in lanes (any q4, n = 4q4 + i)
-        const float l_tot = rows_sum(l_run);
+        // rows of acc are queries 4q4 + i (int8: their sums live in lanes n = 4q4 + i)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int qi = 4 * q4 + i;
-            const float li = __shfl(l_tot, qi, 64);
-            if (active && qi < nq) {
-                const float inv = 1.0f / li;
-                float* o = a.out + (static_cast<int64_t>(q0 + i0 + qi) * Hq + head) * D;
+        for (int k = 0; k < 2; k++) {
+            float li[4];
+            if constexpr (KV == PA_DTYPE_INT8) {
+                const float l_tot = rows_sum(l_run[k]);
 #pragma unroll
-                for (int t = 0; t < NT; t++) o[16 * t + n] = acc[t][i] * inv;
+                for (int i = 0; i < 4; i++) li[i] = __shfl(l_tot, 4 * q4 + i, 64);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) li[i] = acc_l[k][i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int qi = 4 * q4 + i;
+                if (store[k] && qi < nq[k]) {
+                    const float inv = 1.0f / li[i];
+                    float* o = a.out + (static_cast<int64_t>(q0 + i0[k] + qi) * Hq + head[k]) * D;
+#pragma unroll
+                    for (int t = 0; t < NT; t++) o[16 * t + n] = acc[k][t][i] * inv;
+                }
             }
         }
     }
@@ -322,8 +452,8 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void chunked_prefill_kernel(c
 
 template <int D, int KV>
 void launch(const PrefillArgs& a, bool qf32, dim3 grid, hipStream_t s) {
-    if (qf32) chunked_prefill_kernel<D, KV, true><<<grid, 256, 0, s>>>(a);
-    else chunked_prefill_kernel<D, KV, false><<<grid, 256, 0, s>>>(a);
+    if (qf32) chunked_prefill_kernel<D, KV, true><<<grid, kPrefillThreads, 0, s>>>(a);
+    else chunked_prefill_kernel<D, KV, false><<<grid, kPrefillThreads, 0, s>>>(a);
 }
 
 template <int D>
@@ -354,7 +484,6 @@ extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg,
         return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: the cache must be BF16 or INT8");
     if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: int8 cache needs k_scale and v_scale");
-    if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: too many KV heads");
     const uint32_t masks = cfg->flags & (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK);
     if (masks == (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK))
         return pa::set_error(PA_ERROR_INVALID_CONFIG, "pa_chunked_prefill: conflicting mask flags");
@@ -376,7 +505,13 @@ extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg,
     a.mask_mode = (cfg->flags & PA_FLAG_NO_MASK) ? 2 : ((cfg->flags & PA_FLAG_REFERENCE_LITERAL_MASK) ? 1 : 0);
     a.scale = pa::resolve_scale(cfg);
 
-    dim3 grid((max_chunk_len + 15) / 16, cfg->num_kv_heads, num_seqs);
+    a.qtiles_per_wg = a.group >= pa::kPrefillUnits ? 1 : pa::kPrefillUnits / a.group;
+    a.num_qgroups = ((max_chunk_len + 15) / 16 + a.qtiles_per_wg - 1) / a.qtiles_per_wg;
+    const int64_t ng = static_cast<int64_t>(num_seqs) * cfg->num_kv_heads;
+    const int64_t nwg = static_cast<int64_t>(a.num_qgroups) * ((ng + 7) / 8) * 8;
+    if (nwg > 0x7fffffff) return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: grid too large");
+    a.num_groups = static_cast<int32_t>(ng);
+    const dim3 grid(static_cast<uint32_t>(nwg));
     hipStream_t s = pa::native(stream);
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     switch (cfg->head_dim) {
