@@ -171,8 +171,8 @@ def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
     return res
 
 
-def run_c3(timer, stream, steps, warmup, seed):
-    """C3: fused decode of 48 sequences + append of 8 prefill chunks (512 tokens each) + their prefill."""
+def c3_setup(stream, seed):
+    """C3 inputs and the three calls of its layer-step: (workload, decode, chunk append, prefill, prefix lengths)."""
     import torch
 
     w = wl.make_c3()
@@ -205,6 +205,14 @@ def run_c3(timer, stream, steps, warmup, seed):
     def pre():
         pa.chunked_prefill(stream, cfg, out_pre, q_pre, q_start, prefix_g, inp["k_cache"], inp["v_cache"], None,
                            None, tab_g, n_pre, tab.shape[1], L)
+
+    return w, dec, app, pre, P, L, tot
+
+
+def run_c3(timer, stream, steps, warmup, seed):
+    """C3: fused decode of 48 sequences + append of 8 prefill chunks (512 tokens each) + their prefill."""
+    w, dec, app, pre, P, L, tot = c3_setup(stream, seed)
+    n_pre = len(P)
 
     def step():
         dec()
@@ -318,6 +326,8 @@ def main():
                     help="time the headline step only (no two-call comparison, no other configurations, no "
                          "CPU baseline): for profiling")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 measurements")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="time the C3 chunked prefill call only and print its own JSON line: for profiling")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run 10 plain device-to-device copies of this many MiB through pa_memcpy, the "
                          "reference kernel for scaling hardware byte counters")
@@ -342,6 +352,13 @@ def main():
     props = dev.props()
     stream = pa.Stream(dev)
     timer = Timer(dev, stream)
+    if args.only_prefill:
+        w3, _, _, pre, P, L, _ = c3_setup(stream, 3)
+        ms = timer(pre, args.steps, args.warmup)
+        flops = float(4 * w3.num_q_heads * w3.head_dim * np.sum(P * L + L * (L + 1) / 2))
+        print(json.dumps({"mode": "only-prefill", "workload": "C3 chunked prefill", "us": round(ms * 1e3, 3),
+                          "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "steps": args.steps}), flush=True)
+        return
     cfg = config_of(w, args.partition_size)
     S = w.num_seqs
     out, ws, wsb = decode_buffers(w, cfg)
