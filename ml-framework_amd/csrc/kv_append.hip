@@ -37,24 +37,67 @@ __device__ __forceinline__ float load_act(const void* p, bool bf16, int64_t i) {
     return bf16 ? pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
-// fp32 / bf16 caches: one workgroup per token, blockIdx.y selects K (0) or V (1).
+// fp32 / bf16 caches: one workgroup per token, blockIdx.y selects K (0) or V (1). K rows are
+// contiguous per token. A V tile is [D][16]: one token's values are a column, so writing them one
+// by one is D scattered element stores. When the 16 tokens of a block arrive as 16 consecutive
+// slots of this call (a prefill chunk's whole blocks), the 16 workgroups of the block write the
+// tile by dim rows instead (each row one contiguous 16-token run, written in 8- or 16-byte
+// pieces); tokens of partly filled blocks keep the element stores.
 __global__ __launch_bounds__(256) void append_plain_kernel(
     const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
-    const int64_t* __restrict__ slot_mapping, void* __restrict__ k_cache, void* __restrict__ v_cache,
+    const int64_t* __restrict__ slot_mapping, int32_t n_tok, void* __restrict__ k_cache, void* __restrict__ v_cache,
     bool cache_bf16, int32_t num_kv_heads, int32_t head_dim, int64_t capacity) {
     const int i = blockIdx.x;
     const int64_t slot = slot_mapping[i];
     if (slot < 0 || slot >= capacity) return;
-    const void* src = blockIdx.y == 0 ? k_new : v_new;
-    void* dst = blockIdx.y == 0 ? k_cache : v_cache;
+    const bool is_v = blockIdx.y != 0;
+    const void* src = is_v ? v_new : k_new;
+    void* dst = is_v ? v_cache : k_cache;
     const int64_t blk = slot / pa::kBlockSize, off = slot % pa::kBlockSize;
     const int n = num_kv_heads * head_dim;
+    if (is_v) {
+        // Does token i's block arrive whole, as tokens i - off .. i - off + 15 with consecutive slots?
+        __shared__ int s_full;
+        if (threadIdx.x < 64) {
+            const int t = threadIdx.x;
+            const int64_t j = static_cast<int64_t>(i) - off + t;
+            bool ok = true;
+            if (t < pa::kBlockSize) ok = j >= 0 && j < n_tok && slot_mapping[j] == slot - off + t;
+            const bool all = __all(ok);
+            if (t == 0) s_full = all ? 1 : 0;
+        }
+        __syncthreads();
+        if (s_full) {
+            // The 16 workgroups of the block share its tile: workgroup `off` writes dim rows
+            // [off * n / 16, (off + 1) * n / 16) (all heads' rows, row = h * D + d), four threads
+            // per row, each taking 4 consecutive tokens (one 8-byte bf16 / 16-byte fp32 store).
+            const int per = n / pa::kBlockSize;  // rows per workgroup (D is a multiple of 16)
+            const int64_t tok0 = static_cast<int64_t>(i) - off;
+            const int q = threadIdx.x & 3;
+            for (int r = threadIdx.x >> 2; r < per; r += blockDim.x >> 2) {
+                const int idx = static_cast<int>(off) * per + r;
+                const int h = idx / head_dim, d = idx - h * head_dim;
+                float x[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) x[k] = load_act(src, in_bf16, (tok0 + 4 * q + k) * n + idx);
+                const int64_t row = ((blk * num_kv_heads + h) * head_dim + d) * pa::kBlockSize;  // V row d of the tile
+                if (cache_bf16) {
+                    const uint32_t w0 = static_cast<uint32_t>(pa::bf16_trunc(x[0])) | (static_cast<uint32_t>(pa::bf16_trunc(x[1])) << 16);
+                    const uint32_t w1 = static_cast<uint32_t>(pa::bf16_trunc(x[2])) | (static_cast<uint32_t>(pa::bf16_trunc(x[3])) << 16);
+                    reinterpret_cast<uint2*>(static_cast<uint16_t*>(dst) + row)[q] = make_uint2(w0, w1);
+                } else {
+                    reinterpret_cast<float4*>(static_cast<float*>(dst) + row)[q] = make_float4(x[0], x[1], x[2], x[3]);
+                }
+            }
+            return;
+        }
+    }
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         const int h = idx / head_dim, d = idx - h * head_dim;
         const float x = load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
         const int64_t tile = (blk * num_kv_heads + h) * pa::kBlockSize * head_dim;
         // K tiles are [16][D] (token rows); V tiles are [D][16] (dim rows).
-        const int64_t o = blockIdx.y == 0 ? tile + off * head_dim + d : tile + static_cast<int64_t>(d) * pa::kBlockSize + off;
+        const int64_t o = is_v ? tile + static_cast<int64_t>(d) * pa::kBlockSize + off : tile + off * head_dim + d;
         if (cache_bf16) static_cast<uint16_t*>(dst)[o] = pa::bf16_trunc(x);
         else static_cast<float*>(dst)[o] = x;
     }
@@ -195,7 +238,7 @@ pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg, const void* k_ne
     hipStream_t s = pa::native(stream);
     if (cfg->kv_dtype != PA_DTYPE_INT8) {
         dim3 grid(n_tok, 2);
-        append_plain_kernel<<<grid, 256, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, k_cache, v_cache,
+        append_plain_kernel<<<grid, 256, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, k_cache, v_cache,
                                                   cfg->kv_dtype == PA_DTYPE_BF16, cfg->num_kv_heads,
                                                   cfg->head_dim, capacity);
     } else {

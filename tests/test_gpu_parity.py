@@ -110,6 +110,42 @@ def test_append_plain_bit_exact(stream, kv_dtype, q_dtype, D):
     np.testing.assert_array_equal(to_np(gv, cdt), vc)
 
 
+@pytest.mark.parametrize("kv_dtype,q_dtype,D", [(1, 1, 128), (0, 0, 64), (1, 0, 256), (0, 1, 128)])
+def test_append_plain_whole_blocks_bit_exact(stream, kv_dtype, q_dtype, D):
+    """Runs of 16 consecutive slots that fill a block take the kernel's whole-tile V path; the
+    rest (partial runs, a run crossing a block boundary, one broken by an invalid slot or out of
+    order) take the per-token path. Both must write exactly the oracle's bytes."""
+    rng = np.random.default_rng(70 + D + kv_dtype)
+    nb, hkv = 24, 3
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=kv_dtype,
+                         q_dtype=q_dtype, num_blocks=nb)
+    runs = [np.arange(16) + 16 * 3,             # whole block 3
+            np.arange(16) + 16 * 7,             # whole block 7
+            np.arange(5, 16) + 16 * 9,          # tail of block 9
+            np.arange(0, 7) + 16 * 11,          # head of block 11
+            np.arange(16) + 16 * 12 + 5,        # crosses from block 12 into 13
+            np.arange(16) + 16 * 15,            # block 15, one slot invalidated below
+            (np.arange(16) + 16 * 17)[::-1],    # block 17, tokens in reverse order
+            np.arange(16) + 16 * 20]            # whole block 20
+    slots = np.concatenate(runs).astype(np.int64)
+    slots[np.flatnonzero(slots == 16 * 15 + 9)] = -1
+    n = len(slots)
+    src_k = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    src_v = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    if q_dtype == 1:
+        src_k, src_v = orc.bf16_from_f32(src_k), orc.bf16_from_f32(src_v)
+    cdt = np.uint16 if kv_dtype == 1 else np.float32
+    init = rng.standard_normal((nb, hkv, 16, D), dtype=np.float32)
+    kc = orc.bf16_from_f32(init) if kv_dtype == 1 else init.copy()
+    vc = kc.copy()
+    gk, gv = to_gpu(kc), to_gpu(vc)
+    orc.kv_append(cfg, src_k, src_v, slots, kc, vc)
+    pa.kv_append(stream, cfg, to_gpu(src_k), to_gpu(src_v), to_gpu(slots), n, gk, gv)
+    _sync()
+    np.testing.assert_array_equal(to_np(gk, cdt), kc)
+    np.testing.assert_array_equal(to_np(gv, cdt), vc)
+
+
 @pytest.mark.parametrize("D,q_dtype", [(128, 0), (64, 1), (256, 0)])
 def test_append_int8_bit_exact(stream, D, q_dtype):
     """Full-block build, then a decode-style 1-token append with outliers (scale growth and
