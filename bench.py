@@ -313,6 +313,24 @@ def load_traffic():
         return None, None
 
 
+GRAPH_CALLS = 32  # layer-steps per captured graph: one decode step of a 32-layer (Llama-3-8B) model
+
+
+def time_graph_replay(step, timer, stream, steps):
+    """Captures GRAPH_CALLS fused layer-steps into one graph (pa_graph_*) and returns the time per
+    layer-step of its replays on `stream` (the calls reuse one layer's buffers)."""
+    stream.synchronize()
+    g = pa.Graph().capture(stream)
+    for _ in range(GRAPH_CALLS):
+        step()
+    g.end()
+    try:
+        return timer(lambda: g.launch(stream), max(1, steps // GRAPH_CALLS), 2) / GRAPH_CALLS
+    finally:
+        stream.synchronize()
+        g.destroy()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -371,12 +389,16 @@ def main():
 
     step_ms = timer(step, args.steps, args.warmup)
     two_call_ms = float("nan")
+    graph_ms = float("nan")
     extra = None
     if not args.only_step:
         pos = w.context_lens.astype(np.int64) - 1
         inp["slots"] = tensor(w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16)
         two_call_ms = timer(two_call_step, args.steps, args.warmup)
         log(f"[bench] C2 fused step {step_ms * 1e3:.2f} us, two-call step {two_call_ms * 1e3:.2f} us")
+        graph_ms = time_graph_replay(step, timer, stream, args.steps)
+        log(f"[bench] C2 fused step replayed from a captured graph of {GRAPH_CALLS} steps "
+            f"{graph_ms * 1e3:.2f} us per step")
         if not args.no_extra:
             extra = {}
             n = max(20, args.steps // 2)
@@ -450,6 +472,8 @@ def main():
             "us_per_launch": round(step_ms * 1e3, 3),
         },
         "two_call_us_per_layer_step": None if two_call_ms != two_call_ms else round(two_call_ms * 1e3, 3),
+        "graph_replay_us_per_layer_step": None if graph_ms != graph_ms else round(graph_ms * 1e3, 3),
+        "graph_layer_steps_per_replay": GRAPH_CALLS,
         "extra": extra,
         "cpu_baseline": cpu,
         "device": {"name": props.name.decode(), "arch": props.arch.decode(), "cus": props.compute_units},

@@ -96,6 +96,7 @@ typedef struct pa_config {
 typedef struct pa_device pa_device;
 typedef struct pa_stream pa_stream;
 typedef struct pa_event pa_event;
+typedef struct pa_graph pa_graph;
 
 typedef struct pa_device_props {
     char name[256];
@@ -134,6 +135,7 @@ pa_status pa_alloc(pa_device* device, size_t bytes, void** dptr);
 pa_status pa_free(pa_device* device, void* dptr);
 /* Asynchronous on `stream` when it is non-null, otherwise synchronous. */
 pa_status pa_memcpy(void* dst, const void* src, size_t bytes, int32_t kind, pa_stream* stream);
+/* Refuses (PA_ERROR_INVALID_ARGUMENT) a stream that is capturing a graph: no memset is recorded. */
 pa_status pa_memset(void* dst, int32_t value, size_t bytes, pa_stream* stream);
 
 /* ---- streams and events (replace CudaApi.CudaStreamCreate/Destroy/Synchronize and
@@ -152,6 +154,23 @@ pa_status pa_event_record(pa_event* event, pa_stream* stream);
 pa_status pa_event_query(pa_event* event, int32_t* completed);
 pa_status pa_event_synchronize(pa_event* event);
 pa_status pa_event_elapsed_ms(pa_event* start, pa_event* end, float* ms);
+
+/* ---- graphs (replace the CUDA HAL's graph capture and replay: CUDAGraphCapture.BeginCapture /
+ *      EndCapture, HAL/CUDA/Graphs/CUDAGraphCapture.cs:24-61, and CUDAGraph's instantiate /
+ *      Execute / Validate / Dispose, HAL/CUDA/Graphs/CUDAGraph.cs:33-160) --------------------- */
+/* Starts capturing the work enqueued on `stream` (thread-local capture mode, as the reference's
+ * CaptureModeThreadLocal): launches made through this library on `stream` are recorded, not run,
+ * until pa_graph_capture_end. `stream` must be a pa_stream (the null stream cannot capture). */
+pa_status pa_graph_capture_begin(pa_stream* stream);
+/* Ends the capture on `stream` and instantiates the graph; *out_graph replays the recorded work
+ * with the same arguments (the same device buffers, whose contents the caller updates between
+ * replays). On failure the capture is ended and no graph is returned. */
+pa_status pa_graph_capture_end(pa_stream* stream, pa_graph** out_graph);
+/* Replays the graph on `stream` (asynchronous). */
+pa_status pa_graph_launch(pa_graph* graph, pa_stream* stream);
+/* Number of nodes (kernel launches and copies) the graph holds. */
+pa_status pa_graph_node_count(const pa_graph* graph, size_t* count);
+pa_status pa_graph_destroy(pa_graph* graph);
 
 /* ---- paged-attention operators (fill CudaPagedAttentionKernel.ComputePagedAttention,
  *      CudaPagedAttentionKernel.cs:24-36, behind IPagedAttentionKernel,

@@ -25,6 +25,13 @@ struct pa_event {
     hipEvent_t event;
 };
 
+struct pa_graph {
+    int32_t ordinal;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    size_t nodes;
+};
+
 // ---- host-side error plumbing (pa_runtime.hip) -------------------------------------------------
 namespace pa {
 

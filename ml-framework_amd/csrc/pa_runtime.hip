@@ -185,7 +185,16 @@ pa_status pa_memcpy(void* dst, const void* src, size_t bytes, int32_t kind, pa_s
 pa_status pa_memset(void* dst, int32_t value, size_t bytes, pa_stream* stream) {
     if (bytes == 0) return PA_SUCCESS;
     if (!dst) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_memset: null pointer");
-    if (stream) PA_HIP_CHECK(hipMemsetAsync(dst, value, bytes, stream->stream));
+    if (stream) {
+        // Memset nodes in a captured graph have given wrong results on replays after the first
+        // on this platform, so a capturing stream is refused (clear memory with a kernel instead).
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        PA_HIP_CHECK(hipStreamIsCapturing(stream->stream, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_memset: the stream is capturing a graph; "
+                                                        "memset nodes are not recorded");
+        PA_HIP_CHECK(hipMemsetAsync(dst, value, bytes, stream->stream));
+    }
     else PA_HIP_CHECK(hipMemset(dst, value, bytes));
     return PA_SUCCESS;
 }
@@ -292,6 +301,63 @@ pa_status pa_event_synchronize(pa_event* event) {
 pa_status pa_event_elapsed_ms(pa_event* start, pa_event* end, float* ms) {
     if (!start || !end || !ms) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_event_elapsed_ms: null argument");
     PA_HIP_CHECK(hipEventElapsedTime(ms, start->event, end->event));
+    return PA_SUCCESS;
+}
+
+// ---- graphs ------------------------------------------------------------------------------------
+pa_status pa_graph_capture_begin(pa_stream* stream) {
+    if (!stream) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_graph_capture_begin: stream is null");
+    PA_HIP_CHECK(hipStreamBeginCapture(stream->stream, hipStreamCaptureModeThreadLocal));
+    return PA_SUCCESS;
+}
+
+pa_status pa_graph_capture_end(pa_stream* stream, pa_graph** out_graph) {
+    if (!stream || !out_graph) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_graph_capture_end: null argument");
+    *out_graph = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(stream->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return pa::set_hip_error(e, "hipStreamEndCapture");
+    }
+    if (!g) return set_error(PA_ERROR_HIP, "pa_graph_capture_end: the capture produced no graph");
+    size_t nodes = 0;
+    e = hipGraphGetNodes(g, nullptr, &nodes);
+    hipGraphExec_t x = nullptr;
+    if (e == hipSuccess) e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return pa::set_hip_error(e, "hipGraphInstantiate");
+    }
+    auto* pg = new (std::nothrow) pa_graph{stream->ordinal, g, x, nodes};
+    if (!pg) {
+        (void)hipGraphExecDestroy(x);
+        (void)hipGraphDestroy(g);
+        return set_error(PA_ERROR_OUT_OF_MEMORY, "pa_graph_capture_end: host allocation failed");
+    }
+    *out_graph = pg;
+    return PA_SUCCESS;
+}
+
+pa_status pa_graph_launch(pa_graph* graph, pa_stream* stream) {
+    if (!graph) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_graph_launch: graph is null");
+    PA_HIP_CHECK(hipGraphLaunch(graph->exec, pa::native(stream)));
+    return PA_SUCCESS;
+}
+
+pa_status pa_graph_node_count(const pa_graph* graph, size_t* count) {
+    if (!graph || !count) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_graph_node_count: null argument");
+    *count = graph->nodes;
+    return PA_SUCCESS;
+}
+
+pa_status pa_graph_destroy(pa_graph* graph) {
+    if (!graph) return set_error(PA_ERROR_INVALID_ARGUMENT, "pa_graph_destroy: graph is null");
+    hipError_t e = hipGraphExecDestroy(graph->exec);
+    const hipError_t e2 = hipGraphDestroy(graph->graph);
+    delete graph;
+    if (e == hipSuccess) e = e2;
+    if (e != hipSuccess) return pa::set_hip_error(e, "hipGraphDestroy");
     return PA_SUCCESS;
 }
 

@@ -49,6 +49,8 @@ EXPORTS = (
     "pa_stream_synchronize", "pa_stream_wait_event",
     "pa_event_create", "pa_event_destroy", "pa_event_record", "pa_event_query",
     "pa_event_synchronize", "pa_event_elapsed_ms",
+    "pa_graph_capture_begin", "pa_graph_capture_end", "pa_graph_launch", "pa_graph_node_count",
+    "pa_graph_destroy",
     "pa_build_slot_mapping", "pa_kv_append", "pa_decode_workspace_size", "pa_paged_decode",
     "pa_paged_decode_append", "pa_chunked_prefill",
 )
@@ -124,6 +126,11 @@ _SIGNATURES = {
     "pa_event_query": [_P, ctypes.POINTER(_I32)],
     "pa_event_synchronize": [_P],
     "pa_event_elapsed_ms": [_P, _P, ctypes.POINTER(ctypes.c_float)],
+    "pa_graph_capture_begin": [_P],
+    "pa_graph_capture_end": [_P, ctypes.POINTER(_P)],
+    "pa_graph_launch": [_P, _P],
+    "pa_graph_node_count": [_P, ctypes.POINTER(_SZ)],
+    "pa_graph_destroy": [_P],
     "pa_build_slot_mapping": [_P, _CFG, _P, _I32, _P, _P, _P, _I32, _I32, _P],
     "pa_kv_append": [_P, _CFG, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P],
     "pa_decode_workspace_size": [_CFG, _I32, _I32, ctypes.POINTER(_SZ)],
@@ -246,6 +253,38 @@ class Event:
     def destroy(self):
         if self.handle:
             call("pa_event_destroy", self.handle)
+            self.handle = ctypes.c_void_p()
+
+
+class Graph:
+    """A pa_graph: the work enqueued on `stream` between `capture(stream)` and `end()`, replayed
+    with `launch` (mirrors CUDAGraphCapture / CUDAGraph of the reference's CUDA HAL)."""
+
+    def __init__(self):
+        self.handle = ctypes.c_void_p()
+        self._stream = None
+
+    def capture(self, stream: Stream) -> "Graph":
+        call("pa_graph_capture_begin", stream.handle)
+        self._stream = stream
+        return self
+
+    def end(self) -> "Graph":
+        call("pa_graph_capture_end", self._stream.handle, ctypes.byref(self.handle))
+        self._stream = None
+        return self
+
+    def launch(self, stream: Stream):
+        call("pa_graph_launch", self.handle, stream.handle)
+
+    def node_count(self) -> int:
+        n = ctypes.c_size_t()
+        call("pa_graph_node_count", self.handle, ctypes.byref(n))
+        return n.value
+
+    def destroy(self):
+        if self.handle:
+            call("pa_graph_destroy", self.handle)
             self.handle = ctypes.c_void_p()
 
 
