@@ -22,7 +22,7 @@ struct DecodeArgs {
     const int32_t* block_tables;
     const int32_t* context_lens;
     // split-K partials. fp32 kernel: row = (seq * Hq + head) * max_parts + part. MFMA kernel:
-    // row = slot * G + head-in-group, slot = 2 * range + (0: first segment of the range, 1: last).
+    // row = slot * G + head-in-group, slot = 2 * unit + (0: first row portion of the unit, 1: last).
     float* ws_o;  // [rows][D], unnormalised
     float* ws_m;  // [rows]
     float* ws_l;  // [rows]
@@ -40,9 +40,9 @@ struct DecodeArgs {
     int32_t max_parts;
     int32_t part;  // fp32 kernel: partition length in tokens
     // MFMA kernel: the flattened (sequence, KV head, block) list is cut into ranges of
-    // split_blocks blocks (0: ceil(total / split_grid) rounded up to a multiple of 4, at least 4)
+    // split_blocks blocks (0: one range per split_grid / Hkv workers, at least 4 blocks)
     int32_t split_blocks;
-    int32_t split_grid;
+    int32_t split_grid;  // workers (waves) of the launch
     int32_t q_bf16;
     float scale;
 };
@@ -113,13 +113,14 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 }
 
 // Log-sum-exp merge of the partials of one (sequence, KV head): wave w takes query heads
-// w, w + 4, ...; lane l owns dims l, l + 64, ... The loads of 16 partials (max, sum, outputs) are
-// issued together so their latencies overlap. pidx_of(u, g) is the workspace row of partial u of
-// head g of the group.
+// w, w + 4, ...; per head, lane j loads partial j's (max, sum) (64 partials per round), the wave
+// reduces them to the round's max and weighted sum, and the outputs (lane l: dims l, l + 64, ..)
+// are loaded 8 partials at a time, each weighted by the value its lane computed. pidx_of(u, g) is
+// the workspace row of partial u of head g of the group.
 template <int D, typename PidxOf>
 __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
     constexpr int DPL = D / 64;  // dims per lane
-    constexpr int CHUNK = 16;    // partitions whose loads are issued together
+    constexpr int UNROLL = 8;    // partials whose output loads are issued together
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = a.group;
@@ -129,33 +130,39 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
         float o[DPL];
 #pragma unroll
         for (int k = 0; k < DPL; k++) o[k] = 0.0f;
-        // Running log-sum-exp over chunks of partitions; within a chunk every load (m, l and the
-        // partial outputs) is issued before any is used.
-        for (int p0 = 0; p0 < nparts; p0 += CHUNK) {
-            const int cnt = min(CHUNK, nparts - p0);
-            float pm[CHUNK], pl[CHUNK], po[CHUNK][DPL];
-#pragma unroll
-            for (int u = 0; u < CHUNK; u++) {
-                const bool ok = u < cnt;
-                const int64_t pi = pidx_of(p0 + (ok ? u : 0), g);
-                pm[u] = ok ? a.ws_m[pi] : -INFINITY;
-                pl[u] = ok ? a.ws_l[pi] : 0.0f;
-#pragma unroll
-                for (int k = 0; k < DPL; k++) po[u][k] = ok ? a.ws_o[pi * D + lane + 64 * k] : 0.0f;
-            }
-            float cm = M;
-#pragma unroll
-            for (int u = 0; u < CHUNK; u++) cm = fmaxf(cm, pm[u]);
-            const float r = __expf(M - cm);  // rescale of what was accumulated (0 on the first chunk)
-            L *= r;
+        for (int p0 = 0; p0 < nparts; p0 += 64) {
+            const int cnt = min(64, nparts - p0);
+            const bool ok = lane < cnt;
+            const int64_t pi = pidx_of(p0 + (ok ? lane : 0), g);
+            const float pm = ok ? a.ws_m[pi] : -INFINITY;
+            const float pl = ok ? a.ws_l[pi] : 0.0f;
+            const float cm = fmaxf(M, wave_max(pm));  // finite: every partial saw a token
+            const float r = __expf(M - cm);           // rescale of earlier rounds (0 on the first)
+            const float w = ok ? __expf(pm - cm) : 0.0f;
+            L = L * r + wave_sum(pl * w);
 #pragma unroll
             for (int k = 0; k < DPL; k++) o[k] *= r;
+            int u = 0;
+            for (; u + UNROLL <= cnt; u += UNROLL) {
+                float x[UNROLL][DPL];
 #pragma unroll
-            for (int u = 0; u < CHUNK; u++) {
-                const float w = __expf(pm[u] - cm);
-                L += pl[u] * w;
+                for (int j = 0; j < UNROLL; j++) {
+                    const int64_t pj = pidx_of(p0 + u + j, g);
 #pragma unroll
-                for (int k = 0; k < DPL; k++) o[k] += po[u][k] * w;
+                    for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
+                }
+#pragma unroll
+                for (int j = 0; j < UNROLL; j++) {
+                    const float wj = readlane_f(w, u + j);
+#pragma unroll
+                    for (int k = 0; k < DPL; k++) o[k] += x[j][k] * wj;
+                }
+            }
+            for (; u < cnt; u++) {
+                const int64_t pj = pidx_of(p0 + u, g);
+                const float wj = readlane_f(w, u);
+#pragma unroll
+                for (int k = 0; k < DPL; k++) o[k] += a.ws_o[pj * D + lane + 64 * k] * wj;
             }
             M = cm;
         }
@@ -180,18 +187,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArg
 
 // Range length (blocks) of the MFMA kernel's split of the `total` blocks of all sequences (one KV
 // head's worth); the decode and the merge kernel derive the same value from the same arguments.
-// By default the split_grid workgroups form split_grid / Hkv ranges, each range done by Hkv
-// workgroups, one per KV head; ranges hold 4 to 256 blocks (when 256 is not enough, workgroups
-// walk k units each).
+// By default the split_grid workers (waves) form split_grid / Hkv ranges of equal length, each
+// range done by Hkv workers, one per KV head; a range holds at least 4 blocks.
 __device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64_t total) {
     if (a.split_blocks > 0) return a.split_blocks;
     const int64_t nr = a.split_grid >= a.num_kv_heads ? a.split_grid / a.num_kv_heads : 1;
-    // k rounds of nr ranges each, k the fewest that keeps ranges within 256 blocks (a wave's block
-    // ids fit one VGPR); the ranges of the last round are as long as the others', so no workgroup
-    // gets a whole extra range.
-    const int64_t k = (total + 256 * nr - 1) / (256 * nr);
-    int64_t c = (total + k * nr - 1) / (k * nr);
-    c = (c + 3) & ~static_cast<int64_t>(3);
+    const int64_t c = (total + nr - 1) / nr;
     return c < 4 ? 4 : c;
 }
 
@@ -199,7 +200,7 @@ __device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64
 // blocks [R0, R0 + nbr) of the sequence-major block list; its rows were split iff R0 and
 // R0 + nbr - 1 fall in different ranges, and then ranges w1 .. w2 each left one partial per KV
 // head, in unit u = w * Hkv + kvh: slot 2u, except range w1 when the sequence starts inside it (the
-// row is then that unit's last segment, slot 2u + 1).
+// row is then that unit's last row portion, slot 2u + 1).
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const DecodeArgs a, int32_t num_seqs) {
     const int kvh = blockIdx.x, seq = blockIdx.y;
@@ -391,10 +392,15 @@ template <> __device__ __forceinline__ uint32_t buffer_load<uint32_t>(__amdgpu_b
 
 // ---- launchers (one translation unit per kernel family) ----------------------------------------
 constexpr int kMaxPersistentSeqs = 2048;  // per-sequence tables of the persistent kernel (LDS)
-constexpr int kMaxDecodeGrid = 2048;      // persistent workgroups of one MFMA decode launch, at most
+constexpr int kMaxDecodeWorkers = 4096;   // workers (waves) of one MFMA decode launch, at most
+// Workers (waves) per MFMA decode workgroup. Waves sharing a SIMD do not progress evenly (the older
+// one runs ahead and finishes first) but the chip's bandwidth stays in use either way; one 8-wave
+// workgroup per CU instead of two 4-wave ones measured slower.
+__host__ __device__ constexpr int decode_waves(int) { return 4; }
 int device_cus();
-// bf16 / int8 caches; num_seqs < kMaxPersistentSeqs. Launches min(resident workgroups, max_grid)
-// workgroups and records that count in a.split_grid (the merge kernel needs it).
+// bf16 / int8 caches; num_seqs < kMaxPersistentSeqs. Launches the resident workgroups, each of
+// decode_waves(D) independent workers, with no more than kMaxDecodeWorkers and max_units workers
+// in all; records the worker count in a.split_grid (the merge kernel needs it).
 void launch_decode_mfma_d64(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
                             hipStream_t s);
 void launch_decode_mfma_d128(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,

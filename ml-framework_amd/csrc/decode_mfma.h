@@ -1,26 +1,29 @@
-// decode_mfma.h -- the bf16 / int8 paged-decode kernel (MFMA, persistent workgroups, balanced split).
+// decode_mfma.h -- the bf16 / int8 paged-decode kernel (MFMA, persistent waves, balanced split).
 //
 // Work split: the batch's sequences, as runs of 16-token blocks, are laid end to end and cut into
-// ranges of equal block count. A unit is (range, KV head); by default there is one unit per
-// persistent workgroup (with a fixed range length, workgroups walk units with a stride of
-// gridDim.x). A range covers the tail of one sequence, whole sequences and the head of another;
-// each piece, for the unit's KV head, is a segment. A segment that is a whole row (sequence, KV
-// head) writes the normalised output directly; the (at most two) partial segments of a unit write
-// (max, sum, unnormalised O) to workspace slots 2 * unit + {0: first, 1: last}, and
-// paged_decode_merge_split_kernel combines the slots of every split row. Every workgroup thus
-// streams the same number of K/V bytes whatever the mix of context lengths, and the Hkv
-// workgroups of a range read the same physical blocks at about the same time.
+// ranges of equal block count. A unit is (range, KV head) and belongs to one wave (a worker): the
+// launch's waves are numbered blockIdx.x * 4 + wave, and unit u = range * Hkv + kvh goes to worker
+// u (workers walk units with a stride of the worker count when there are more units). The 4 waves
+// of a workgroup thus take 4 KV heads of one range (or 4 ranges when Hkv is 1 or 2) and read
+// neighbouring bytes of the same physical blocks. A range covers the tail of one sequence, whole
+// sequences and the head of another; each part, for the unit's KV head, is a row portion. A
+// portion that is a whole row (sequence, KV head) writes the normalised output directly; the (at
+// most two) partial portions of a unit write (max, sum, unnormalised O) to workspace slots
+// 2 * unit + {0: first, 1: last}, and paged_decode_merge_split_kernel combines the slots of every
+// split row. Every worker streams the same number of K/V bytes whatever the mix of context lengths,
+// and no wave ever waits for another: there is no barrier after the prefix table is built.
 //
-// Per segment (at most 256 blocks), its blocks are dealt to the 4 waves round-robin (block
-// b0 + wave + 4j), so a wave's block ids fit one VGPR (lane j: its j-th block). The next segment's
-// ids are loaded while the current one streams, so a segment starts with one memory round trip.
+// A portion is streamed in pieces of at most 64 blocks (lane j holds the id of the piece's block
+// j); the running (max, sum, O) carry over from piece to piece and are written when the portion
+// ends. The next piece's ids are loaded while the current one streams, so a piece starts with one
+// memory round trip.
 //
-// Per block and wave: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads
-// padded to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16
-// with P split into bf16 high and low parts (~16 significant bits). The score layout the first
-// MFMA leaves in registers (lane = (token group q4, head n)) is the A-operand layout of the second,
-// so P never leaves registers. Three rotating register buffers keep two blocks in flight while a
-// third is consumed. The four waves' (max, sum, O) are combined through LDS at the segment's end.
+// Per block: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads padded
+// to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
+// split into bf16 high and low parts (~16 significant bits). The score layout the first MFMA
+// leaves in registers (lane = (token group q4, head n)) is the A-operand layout of the second, so
+// P never leaves registers. Three rotating register buffers keep two blocks in flight while a
+// third is consumed.
 #pragma once
 
 #include "decode_common.h"
@@ -33,35 +36,52 @@ namespace pa {
 constexpr float kRescaleThreshold = 8.0f;
 
 struct MfmaShared {
-    float m[4][16];
-    float l[4][16];
     int pref[kMaxPersistentSeqs + 1];  // blocks (per KV head row) before sequence s
     int lens[kMaxPersistentSeqs];      // clamped context length of sequence s
 };
 
-// Blocks [b0, b1) of row (seq, kvh); slot < 0: the whole row (final output), else workspace slot.
-struct Segment {
+// Blocks [b0, b1) of row (seq, kvh), at most kPieceBlocks of them. slot < 0: the portion the
+// piece belongs to is the whole row (final output), else its workspace slot; last: the piece ends
+// the portion (its results are written).
+struct Piece {
     int seq, kvh, b0, b1, T, slot;
+    bool last;
 };
 
-constexpr int kMaxSegmentBlocks = 256;  // 64 per wave: one block id per lane
+constexpr int kPieceBlocks = 64;  // one block id per lane
 
-// Ids of this wave's blocks of a segment: lane j holds block b0 + wave + 4j (-1 beyond the
-// segment). Ids are range-checked where they are used (valid_bid): a check here would make the
-// wave wait for the table load at the point of issue instead of when the id is needed.
-__device__ __forceinline__ int segment_ids(const DecodeArgs& a, const Segment& g, int wave, int lane) {
-    const int b = g.b0 + wave + 4 * lane;
+// Ids of a piece's blocks: lane j holds block b0 + j (-1 beyond the piece). Ids are range-checked
+// where they are used (valid_bid): a check here would make the wave wait for the table load at the
+// point of issue instead of when the id is needed.
+__device__ __forceinline__ int piece_ids(const DecodeArgs& a, const Piece& g, int lane) {
+    const int b = g.b0 + lane;
     int id = -1;
     if (b < g.b1) id = a.block_tables[static_cast<int64_t>(g.seq) * a.max_blocks_per_seq + b];
     return id;
 }
 __device__ __forceinline__ int valid_bid(const DecodeArgs& a, int id) { return id < a.num_blocks ? id : -1; }
 
-// One segment. Called by all 256 threads of a workgroup; my_bid = segment_ids(..). prefetch_next()
-// is called once, after the segment's first loads, to start the next segment's id loads.
+// Running (max, sum, O) of one row portion; lane (q4, n): head n's max, its share of head n's sum,
+// and O rows 4q4 .. 4q4 + 3 of dims 16t + n.
+template <int NT>
+struct RowState {
+    float m_run;  // reference max of head n (exceeded by at most kRescaleThreshold)
+    float l_run;  // this lane's share of the running sum of head n
+    f32x4_t acc[NT];
+    __device__ __forceinline__ void reset() {
+        m_run = -INFINITY;
+        l_run = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+};
+
+// One piece, streamed by one wave; my_bid = piece_ids(..). prefetch_next() is called once, after
+// the piece's first loads, to start the next piece's id loads. s_new: this wave's LDS staging of
+// the appended token (2 * D floats).
 template <int D, int KV, bool QF32, bool APPEND, typename Prefetch>
-__device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment& g, int my_bid, MfmaShared& sh,
-                                             float (*s_x)[D][16], Prefetch&& prefetch_next) {
+__device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, int my_bid, RowState<D / 16>& st,
+                                           float* s_new, Prefetch&& prefetch_next) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
@@ -69,36 +89,32 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment&
     constexpr int TILE = 16 * D;   // elements per (block, KV head) tile
     constexpr int NPL = D / 64;    // appended-token values per lane
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4;  // token group (QK C rows) / k group of the MFMA operands
     const int n = lane & 15;   // head column of S^T / row of P / dim within a PV tile
     const int G = a.group, Hkv = a.num_kv_heads;
     const int seq = g.seq, kvh = g.kvh, T = g.T;
-    const int nblk = g.b1 - g.b0;
-    const int nb = nblk > wave ? (nblk - wave + 3) / 4 : 0;  // this wave's blocks
+    const int nb = g.b1 - g.b0;
     const int nbrow = (T + 15) / 16;
 
-    // Loads issued at the segment's start, in this order: its first two K/V blocks, the next
-    // segment's block ids (prefetch callback), then Q, the int8 block scales and the appended token.
+    // Loads issued at the piece's start, in this order: its first two K/V blocks, the next
+    // piece's block ids (prefetch callback), then Q, the int8 block scales and the appended token.
     // Memory returns in order, so the K/V requests go out first; none of the other values is
     // used right after its load (that would stall the wave on the load's latency).
     float my_ks = 0.0f, my_vs = 0.0f;  // int8: scales of this lane's block
-    // Fused append: the row's last block belongs to wave (rel & 3) at iteration rel >> 2 of the
-    // segment that ends the row. That wave fetches the new token (lane l: dims l*NPL ..) and, for
-    // int8, the block's running statistics; the token's raw bits (fp32, or bf16 packed two per
-    // word) are decoded only at the patch.
+    // Fused append: the row's last block is entry nbrow - 1 - b0 of the piece that ends the row.
+    // Its wave fetches the new token (lane l: dims l*NPL ..) and, for int8, the block's running
+    // statistics; the token's raw bits (fp32, or bf16 packed two per word) are decoded only at the
+    // patch.
     constexpr int NW = QF32 ? NPL : (NPL + 1) / 2;
     int j_app = -1;
     uint32_t nk_raw[NW], nv_raw[NW];
     Int8Stats old{};
     if constexpr (APPEND) {
-        const int rel = nbrow - 1 - g.b0;
-        if (g.b1 == nbrow && (rel & 3) == wave) j_app = rel >> 2;  // always this wave's last block
+        if (g.b1 == nbrow) j_app = nbrow - 1 - g.b0;  // always the piece's last block
     }
-    // The appending wave consumes its blocks starting with that last one (iteration 0 takes list
-    // entry j_app, iteration j takes entry j - 1): the patch then happens while the pipeline fills
-    // instead of at the end of the segment, where every other wave would wait for it.
+    // That piece consumes its blocks starting with the last one (iteration 0 takes list entry
+    // j_app, iteration j takes entry j - 1): the patch then happens while the pipeline fills.
     const bool rot = APPEND && j_app > 0;
     auto entry = [&](int j) { return rot ? (j == 0 ? j_app : j - 1) : j; };
     auto new_val = [&](const uint32_t (&raw)[NW], int e) -> float {
@@ -189,11 +205,9 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment&
         for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
     };
 
-    float m_run = -INFINITY;  // reference max of head n (exceeded by at most kRescaleThreshold)
-    float l_run = 0.0f;       // this lane's share of the running sum of head n
-    f32x4_t acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float& m_run = st.m_run;
+    float& l_run = st.l_run;
+    f32x4_t(&acc)[NT] = st.acc;
 
     auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
         const int e = entry(j);
@@ -205,9 +219,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment&
         }
         if constexpr (APPEND) {
             if (e == j_app && bid >= 0) {
-                // Stage the new token in LDS (free during streaming: the previous segment's
-                // combine ended with a barrier, this one's starts with one), then patch the tile.
-                float* s_new = &s_x[0][0][0];
+                // Stage the new token in this wave's LDS area, then patch the tile.
                 // The empty asm keeps the decoding here: hoisted out of the loop, it would wait
                 // for the token's loads before the first block.
                 uint32_t kw[NW], vw[NW];
@@ -241,7 +253,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment&
             s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
             if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
         }
-        const int tbase = (g.b0 + wave + 4 * e) * 16 + 4 * q4;
+        const int tbase = (g.b0 + e) * 16 + 4 * q4;
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -314,91 +326,54 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, const Segment&
         }
     }
 
-    // ---- combine the 4 waves: weights exp(m_w - M) per head, then a 2-level tree in LDS ----
-    const float l_tot = rows_sum(l_run);
-    if (q4 == 0) {
-        sh.m[wave][n] = m_run;
-        sh.l[wave][n] = l_tot;
-    }
-    __syncthreads();
-    float M[4], f_own[4];
+    if (!g.last) return;
+    // ---- the portion ends: write it (lane (q4, n) holds O rows 4q4 .. 4q4 + 3, dims 16t + n) ----
+    const float l_tot = rows_sum(l_run);  // head n's sum, in every lane of column n
+    float M[4], L[4];                     // of head 4q4 + i, read from lane 4q4 + i (column 4q4 + i)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int h = 4 * q4 + i;
-        M[i] = fmaxf(fmaxf(sh.m[0][h], sh.m[1][h]), fmaxf(sh.m[2][h], sh.m[3][h]));
-        f_own[i] = __expf(sh.m[wave][h] - M[i]);  // 0 for a wave that saw no block
+        M[i] = __shfl(m_run, 4 * q4 + i, 64);
+        L[i] = __shfl(l_tot, 4 * q4 + i, 64);
     }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[t][i] *= f_own[i];
-    // acc[t] holds rows 4q4..4q4+3 of dim 16t+n: one 16-byte LDS store in the [dim][row] layout.
-    if (wave >= 2) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) *reinterpret_cast<f32x4_t*>(&s_x[wave - 2][16 * t + n][4 * q4]) = acc[t];
-    }
-    __syncthreads();
-    if (wave < 2) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            f32x4_t* slot = reinterpret_cast<f32x4_t*>(&s_x[wave][16 * t + n][4 * q4]);
-            acc[t] += *slot;
-            if (wave == 1) *slot = acc[t];
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
-        float L[4];
+    if (4 * q4 < G) {
+        const int64_t row0 = static_cast<int64_t>(seq) * Hkv * G + kvh * G;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int h = 4 * q4 + i;
-            L[i] = 0.0f;
+            if (h >= G) break;
+            if (g.slot < 0) {
+                const float inv = 1.0f / L[i];
 #pragma unroll
-            for (int w = 0; w < 4; w++) L[i] += sh.l[w][h] * __expf(sh.m[w][h] - M[i]);
-        }
+                for (int t = 0; t < NT; t++) a.out[(row0 + h) * D + 16 * t + n] = acc[t][i] * inv;
+            } else {
+                const int64_t pidx = static_cast<int64_t>(g.slot) * G + h;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const f32x4_t other = *reinterpret_cast<const f32x4_t*>(&s_x[1][16 * t + n][4 * q4]);
-            acc[t] += other;
-        }
-        if (4 * q4 < G) {
-            const int64_t row0 = static_cast<int64_t>(seq) * Hkv * G + kvh * G;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int h = 4 * q4 + i;
-                if (h >= G) break;
-                if (g.slot < 0) {
-                    const float inv = 1.0f / L[i];
-#pragma unroll
-                    for (int t = 0; t < NT; t++) a.out[(row0 + h) * D + 16 * t + n] = acc[t][i] * inv;
-                } else {
-                    const int64_t pidx = static_cast<int64_t>(g.slot) * G + h;
-#pragma unroll
-                    for (int t = 0; t < NT; t++) a.ws_o[pidx * D + 16 * t + n] = acc[t][i];
-                    if (n == 0) {
-                        a.ws_m[pidx] = M[i];
-                        a.ws_l[pidx] = L[i];
-                    }
+                for (int t = 0; t < NT; t++) a.ws_o[pidx * D + 16 * t + n] = acc[t][i];
+                if (n == 0) {
+                    a.ws_m[pidx] = M[i];
+                    a.ws_l[pidx] = L[i];
                 }
             }
         }
     }
-    __syncthreads();  // LDS reuse by the next segment
+    st.reset();
 }
 
 // Persistent decode kernel over at most kMaxPersistentSeqs - 1 sequences.
 template <int D, int KV, bool QF32, bool APPEND>
-__global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a,
-                                                                                          int32_t num_seqs) {
+__global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a,
+                                                                                             int32_t num_seqs) {
+    constexpr int WAVES = decode_waves(D);
+    constexpr int THREADS = 64 * WAVES;
     __shared__ MfmaShared sh;
-    __shared__ float s_x[2][D][16];
+    __shared__ float s_app[WAVES][2 * D];  // per wave: the appended token's K and V values
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Blocks per row of each sequence; exclusive prefix over sequences, built by the workgroup.
     // All PER lengths are loaded before any is used, so the loads overlap (a use between them would
     // serialise PER memory round trips).
-    constexpr int PER = (kMaxPersistentSeqs + 255) / 256;
+    constexpr int PER = (kMaxPersistentSeqs + THREADS - 1) / THREADS;
     int raw[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) raw[k] = a.context_lens[min(tid * PER + k, num_seqs - 1)];
@@ -444,51 +419,76 @@ __global__ __launch_bounds__(256, D > 128 ? 1 : 2) void paged_decode_mfma_persis
     for (int s = blockIdx.x; s < num_seqs; s += gridDim.x) {
         if (sh.lens[s] > 0) continue;
         const int n = Hkv * a.group * D;
-        for (int idx = tid; idx < n; idx += 256) a.out[static_cast<int64_t>(s) * n + idx] = 0.0f;
+        for (int idx = tid; idx < n; idx += THREADS) a.out[static_cast<int64_t>(s) * n + idx] = 0.0f;
     }
 
     // Units u = range * Hkv + kvh; unit u walks blocks [range * C, (range + 1) * C) of the
-    // sequence-major block list for KV head kvh. Workgroups u .. u + Hkv - 1 run together and read
-    // the same physical blocks (all KV heads of a block are one contiguous Hkv * 16 * D run).
+    // sequence-major block list for KV head kvh, on worker u (mod the worker count W). Workers
+    // u .. u + Hkv - 1 run together and read the same physical blocks (all KV heads of a block are
+    // one contiguous Hkv * 16 * D run). From here on every wave works alone.
     const int64_t total = sh.pref[num_seqs];
     if (total == 0) return;
+    const int64_t W = a.split_grid;
     const int64_t C = split_range_blocks(a, total);
     const int64_t units = (total + C - 1) / C * Hkv;
-    int64_t u = blockIdx.x;
-    if (u >= units) return;
+    int64_t u = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+    if (u >= W || u >= units) return;
     int64_t r = u / Hkv;
     int kvh = static_cast<int>(u - r * Hkv);
     int64_t p = r * C, end = min(total, p + C);
-    int seq = 0;  // scanned forward while positions increase
-    auto next_segment = [&](Segment& g) -> bool {
-        if (p >= end) {
-            u += gridDim.x;
-            if (u >= units) return false;
-            r = u / Hkv;
-            kvh = static_cast<int>(u - r * Hkv);
-            p = r * C;
-            end = min(total, p + C);
-            if (sh.pref[seq] > p) seq = 0;
+    // Sequence holding block position pos (pref[s] <= pos < pref[s + 1]; pos < total): a binary
+    // search, so a worker whose range lies far into the batch does not start late behind a chain of
+    // dependent LDS reads.
+    auto locate = [&](int64_t pos) {
+        int lo = 0, hi = num_seqs;  // pref[lo] <= pos < pref[hi]
+        while (hi - lo > 1) {
+            const int h = (lo + hi) >> 1;
+            if (sh.pref[h] <= pos) lo = h;
+            else hi = h;
         }
-        while (sh.pref[seq + 1] <= p) seq++;
-        const int nbr = sh.pref[seq + 1] - sh.pref[seq];
+        return lo;
+    };
+    int seq = locate(p);  // then scanned forward while positions increase
+    bool mid = false;     // the next piece continues the current row portion
+    int prow_end = 0;     // block (within the row) where the unit's portion of the row ends
+    int pslot = -1;       // the portion's output: -1 the whole row, else its workspace slot
+    auto next_piece = [&](Piece& g) -> bool {
+        if (!mid) {
+            if (p >= end) {
+                u += W;
+                if (u >= units) return false;
+                r = u / Hkv;
+                kvh = static_cast<int>(u - r * Hkv);
+                p = r * C;
+                end = min(total, p + C);
+                seq = locate(p);
+            }
+            while (sh.pref[seq + 1] <= p) seq++;
+            const int nbr = sh.pref[seq + 1] - sh.pref[seq];
+            const int pb0 = static_cast<int>(p - sh.pref[seq]);
+            prow_end = static_cast<int>(min(static_cast<int64_t>(nbr), pb0 + (end - p)));
+            pslot = (pb0 == 0 && prow_end == nbr) ? -1 : static_cast<int>(2 * u + (p == r * C ? 0 : 1));
+        }
         const int b0 = static_cast<int>(p - sh.pref[seq]);
-        const int b1 = static_cast<int>(min(static_cast<int64_t>(nbr), b0 + (end - p)));
-        const int slot = (b0 == 0 && b1 == nbr) ? -1 : static_cast<int>(2 * u + (p == r * C ? 0 : 1));
-        g = Segment{seq, kvh, b0, b1, sh.lens[seq], slot};
+        const int b1 = min(prow_end, b0 + kPieceBlocks);
+        mid = b1 < prow_end;
+        g = Piece{seq, kvh, b0, b1, sh.lens[seq], pslot, !mid};
         p += b1 - b0;
         return true;
     };
-    Segment cur;
-    next_segment(cur);
-    int cur_ids = segment_ids(a, cur, wave, lane);
+    RowState<D / 16> st;
+    st.reset();
+    float* s_new = &s_app[wave][0];
+    Piece cur;
+    next_piece(cur);
+    int cur_ids = piece_ids(a, cur, lane);
     for (;;) {
-        Segment nxt;
+        Piece nxt;
         bool has_next = false;
         int nxt_ids = -1;
-        mfma_segment<D, KV, QF32, APPEND>(a, cur, cur_ids, sh, s_x, [&]() {
-            has_next = next_segment(nxt);
-            if (has_next) nxt_ids = segment_ids(a, nxt, wave, lane);  // in flight during this segment
+        mfma_piece<D, KV, QF32, APPEND>(a, cur, cur_ids, st, s_new, [&]() {
+            has_next = next_piece(nxt);
+            if (has_next) nxt_ids = piece_ids(a, nxt, lane);  // in flight during this piece
         });
         if (!has_next) break;
         cur = nxt;

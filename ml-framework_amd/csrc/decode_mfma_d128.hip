@@ -8,18 +8,20 @@ template <int D, int KV, bool QF32, bool APPEND>
 void launch_one(DecodeArgs& a, int num_seqs, int64_t max_grid, hipStream_t s) {
     auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND>;
     // Resident workgroups per CU for this instance (queried once; read-only afterwards).
+    constexpr int waves = decode_waves(D);
     static const int per_cu = [&] {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, 0) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 64 * waves, 0) != hipSuccess || n < 1) n = 1;
         return n;
     }();
-    int64_t nwg = static_cast<int64_t>(device_cus()) * per_cu;
-    if (nwg > kMaxDecodeGrid) nwg = kMaxDecodeGrid;
-    if (nwg >= a.num_kv_heads) nwg -= nwg % a.num_kv_heads;  // whole ranges (one unit per KV head)
-    if (nwg > max_grid) nwg = max_grid;
-    if (nwg < 1) nwg = 1;
-    a.split_grid = static_cast<int32_t>(nwg);
-    kern<<<static_cast<unsigned>(nwg), 256, 0, s>>>(a, num_seqs);
+    int64_t workers = static_cast<int64_t>(device_cus()) * per_cu * waves;
+    if (workers > kMaxDecodeWorkers) workers = kMaxDecodeWorkers;
+    if (workers >= a.num_kv_heads) workers -= workers % a.num_kv_heads;  // whole ranges (one unit per KV head)
+    if (workers > max_grid) workers = max_grid;
+    if (workers < 1) workers = 1;
+    a.split_grid = static_cast<int32_t>(workers);
+    const int64_t nwg = (workers + waves - 1) / waves;
+    kern<<<static_cast<unsigned>(nwg), 64 * waves, 0, s>>>(a, num_seqs);
 }
 
 template <int KV, bool QF32>

@@ -61,18 +61,18 @@ int resolve_part(const pa_config* cfg, std::string* err) {
 }
 
 // Units (range, KV head) an MFMA launch over (at most) this shape can produce: the bound the
-// workspace is sized for. By default ranges hold 4 to 256 blocks and there are at most
-// k * nr <= blocks / 256 + nr of them (nr <= kMaxDecodeGrid / Hkv ranges per round).
+// workspace is sized for. By default there are at most nr ranges (nr = workers / Hkv, workers <=
+// kMaxDecodeWorkers) of at least 4 blocks each.
 int64_t mfma_max_units(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
     const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
     const int64_t wmax = seqs * ((static_cast<int64_t>(max_len) + 15) / 16);
     const int64_t hkv = cfg->num_kv_heads;
     if (wmax <= 0) return 0;
     if (part > 0) return (wmax + part / 16 - 1) / (part / 16) * hkv;
-    const int64_t nr = pa::kMaxDecodeGrid >= hkv ? pa::kMaxDecodeGrid / hkv : 1;
-    const int64_t by_rounds = (wmax + 255) / 256 + nr;
+    const int64_t workers = pa::kMaxDecodeWorkers;
+    const int64_t nr = workers >= hkv ? workers / hkv : 1;
     const int64_t by_min_len = (wmax + 3) / 4;
-    return (by_rounds < by_min_len ? by_rounds : by_min_len) * hkv;
+    return (nr < by_min_len ? nr : by_min_len) * hkv;
 }
 
 size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
