@@ -115,12 +115,12 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 // Log-sum-exp merge of the partials of one (sequence, KV head): wave w takes query heads
 // w, w + 4, ...; per head, lane j loads partial j's (max, sum) (64 partials per round), the wave
 // reduces them to the round's max and weighted sum, and the outputs (lane l: dims l, l + 64, ..)
-// are loaded 8 partials at a time, each weighted by the value its lane computed. pidx_of(u, g) is
+// are loaded 16 partials at a time, each weighted by the value its lane computed. pidx_of(u, g) is
 // the workspace row of partial u of head g of the group.
 template <int D, typename PidxOf>
 __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
     constexpr int DPL = D / 64;  // dims per lane
-    constexpr int UNROLL = 8;    // partials whose output loads are issued together
+    constexpr int UNROLL = 16;   // partials whose output loads are issued together
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = a.group;
@@ -142,27 +142,27 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
             L = L * r + wave_sum(pl * w);
 #pragma unroll
             for (int k = 0; k < DPL; k++) o[k] *= r;
-            int u = 0;
-            for (; u + UNROLL <= cnt; u += UNROLL) {
+            for (int u = 0; u < cnt; u += UNROLL) {
+                // Every load of a batch is issued before any is used; past cnt (uniform) nothing
+                // is loaded and the weight read is lane 63's or beyond-cnt zero, times zero.
                 float x[UNROLL][DPL];
 #pragma unroll
                 for (int j = 0; j < UNROLL; j++) {
-                    const int64_t pj = pidx_of(p0 + u + j, g);
+                    if (u + j < cnt) {
+                        const int64_t pj = pidx_of(p0 + u + j, g);
 #pragma unroll
-                    for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
+                        for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < DPL; k++) x[j][k] = 0.0f;
+                    }
                 }
 #pragma unroll
                 for (int j = 0; j < UNROLL; j++) {
-                    const float wj = readlane_f(w, u + j);
+                    const float wj = readlane_f(w, min(u + j, 63));
 #pragma unroll
                     for (int k = 0; k < DPL; k++) o[k] += x[j][k] * wj;
                 }
-            }
-            for (; u < cnt; u++) {
-                const int64_t pj = pidx_of(p0 + u, g);
-                const float wj = readlane_f(w, u);
-#pragma unroll
-                for (int k = 0; k < DPL; k++) o[k] += a.ws_o[pj * D + lane + 64 * k] * wj;
             }
             M = cm;
         }
