@@ -230,6 +230,13 @@ __device__ __forceinline__ s16x4_t v_operand(const uint32_t& r) {
     return __builtin_bit_cast(s16x4_t, p);
 }
 
+// First of the 8 consecutive dims of K slab sl (32 dims of one QK MFMA) that lane group q4 feeds
+// in the decode kernel: the dot product does not depend on which dims go to which MFMA k slot as
+// long as K and Q agree, so each lane group takes a contiguous D / 4 dims over its slabs and its
+// piece of a K row is one run (two 16-byte loads for int8 D 128 instead of four 8-byte ones).
+template <int D>
+__device__ __forceinline__ int k_dim0(int sl, int q4) { return (D / 4) * q4 + 8 * sl; }
+
 // ---- fused append: the new token (row r of the sequence's last block) enters the owning wave's
 // registers and the cache. Values and cache bytes are those of pa_kv_append for that one token.
 __device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
@@ -248,7 +255,7 @@ __device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t ti
     if (n == r) {  // K row r: dims 32s + 8q4 .. +8 of this lane
 #pragma unroll
         for (int sl = 0; sl < NSLAB; sl++) {
-            const int d0 = 32 * sl + 8 * q4;
+            const int d0 = k_dim0<D>(sl, q4);
             const float* x = s_new + d0;
             const uint4 v = make_uint4(pack_bf16_trunc(x[0], x[1]), pack_bf16_trunc(x[2], x[3]),
                                        pack_bf16_trunc(x[4], x[5]), pack_bf16_trunc(x[6], x[7]));
@@ -304,7 +311,7 @@ __device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t ti
         for (int sl = 0; sl < NSLAB; sl++)
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                x[sl][e] = n == r ? s_new[32 * sl + 8 * q4 + e] : 0.0f;
+                x[sl][e] = n == r ? s_new[k_dim0<D>(sl, q4) + e] : 0.0f;
                 const float ax = fabsf(x[sl][e]);
                 amax = ax > amax ? ax : amax;
             }
@@ -325,7 +332,7 @@ __device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t ti
                 w[e >> 2] = with_code(w[e >> 2], e & 3, c);
             }
             kr[sl] = make_uint2(w[0], w[1]);
-            if (grow || n == r) *reinterpret_cast<uint2*>(kc + tile + n * D + 32 * sl + 8 * q4) = kr[sl];
+            if (grow || n == r) *reinterpret_cast<uint2*>(kc + tile + n * D + k_dim0<D>(sl, q4)) = kr[sl];
         }
         if (lane == 0 && (fresh || grow)) {
             a.k_absmax[sidx] = amax;

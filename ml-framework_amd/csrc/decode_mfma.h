@@ -122,14 +122,14 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         else if constexpr (NPL == 1) return __uint_as_float(raw[0] << 16);
         else return __uint_as_float((e & 1) ? (raw[e >> 1] & 0xffff0000u) : (raw[e >> 1] << 16));
     };
-    // Q^T operand: lane (q4, n) holds head n, dims 32s + 8q4 .. +8 (zero rows for n >= G).
+    // Q^T operand: lane (q4, n) holds head n, dims k_dim0(s, q4) .. +8 of slab s (zero rows for n >= G).
     bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
     auto side_loads = [&]() {
         const bool hv = n < G;
         const int64_t qrow = (static_cast<int64_t>(seq) * Hkv * G + kvh * G + (hv ? n : 0)) * D;
 #pragma unroll
         for (int s = 0; s < NSLAB; s++) {
-            const int d0 = 32 * s + 8 * q4;
+            const int d0 = k_dim0<D>(s, q4);
             if constexpr (QF32) {
                 const float* qp = static_cast<const float*>(a.q) + qrow + d0;
                 float x[8];
@@ -185,7 +185,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     const char* vc = static_cast<const char*>(a.v_cache);
     using KR = typename Raw::K;
     using VR = typename Raw::V;
-    const int k_lane_off = (n * D + 8 * q4) * ELT;   // K row n, dims 8q4 .. (+32 per slab)
+    const int k_lane_off = (n * D + k_dim0<D>(0, q4)) * ELT;  // K row n, D / 4 dims from here
     const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
     // Loads go through per-block buffer descriptors: a block past the wave's list or with an
     // invalid id gets a zero-sized descriptor, so its loads return zeros without touching memory.
@@ -199,8 +199,17 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
         const __amdgpu_buffer_rsrc_t rv =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
+        if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
 #pragma unroll
-        for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR>(rk, k_lane_off + 32 * s * ELT);
+            for (int s = 0; s < NSLAB; s += 2) {
+                const uint4 w = buffer_load<uint4>(rk, k_lane_off + 8 * s);
+                kr[s] = make_uint2(w.x, w.y);
+                kr[s + 1] = make_uint2(w.z, w.w);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR>(rk, k_lane_off + 8 * s * ELT);
+        }
 #pragma unroll
         for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
     };
