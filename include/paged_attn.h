@@ -237,11 +237,12 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
  * (k_new/v_new [num_seqs][num_kv_heads][head_dim] of cfg->q_dtype) into the cache, then runs
  * pa_paged_decode. Cache bytes, int8 scales and absmax after the call are exactly those of
  * pa_kv_append with slot_mapping[s] = block_tables[s][(T-1)/16] * 16 + (T-1) % 16 followed by
- * pa_paged_decode; for bf16/int8 caches both happen in one kernel (the workgroup that owns a
- * sequence's last block patches the new token into its registers and the cache). No reference
- * counterpart: the reference appends (PagedAttentionLayer.UpdateKVCache, Layers/
- * PagedAttentionLayer.cs:244-296) and decodes (DecodeOrchestrator.ComputeDecodeAttention,
- * Phases/DecodeOrchestrator.cs:64-80) in two steps; this is those two steps in one launch.
+ * pa_paged_decode; for bf16 caches both happen in one kernel (the wave that owns a sequence's
+ * last block patches the new token into its registers and the cache), for int8 caches the
+ * quantising append is a launch of its own ahead of the decode, and for fp32 caches a plain
+ * copy kernel. No reference counterpart: the reference appends (PagedAttentionLayer.UpdateKVCache,
+ * Layers/PagedAttentionLayer.cs:244-296) and decodes (DecodeOrchestrator.ComputeDecodeAttention,
+ * Phases/DecodeOrchestrator.cs:64-80) in two steps; this is those two steps in one call.
  * Sequences with context_len <= 0 append nothing and produce zeros. */
 pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
                                  const void* k_new, const void* v_new, void* k_cache, void* v_cache,

@@ -278,111 +278,6 @@ __device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t ti
     }
 }
 
-__device__ __forceinline__ int code_at(uint32_t w, int k) { return static_cast<int32_t>(w << (24 - 8 * k)) >> 24; }
-__device__ __forceinline__ uint32_t with_code(uint32_t w, int k, int8_t c) {
-    return (w & ~(0xffu << (8 * k))) | (static_cast<uint32_t>(static_cast<uint8_t>(c)) << (8 * k));
-}
-
-// Running statistics of one (block, KV head) before the append.
-struct Int8Stats {
-    float k_absmax, k_scale, v_absmax, v_scale;
-};
-
-// int8: the owning wave holds the whole (block, head) tile in registers (K: 8 codes per lane per
-// 32-dim slab, V: 4 codes per lane per 16-dim tile), so the scale growth and requantisation of
-// pa_kv_append run in place. Returns the tile's K and V scales after the append.
-template <int D>
-__device__ __forceinline__ void append_int8_regs(const DecodeArgs& a, int64_t tile, int64_t sidx, const float* s_new,
-                                                 int r, int q4, int n, const Int8Stats& old, uint2 (&kr)[D / 32],
-                                                 uint32_t (&vr)[D / 16], float& k_scale_out, float& v_scale_out) {
-#pragma clang fp contract(off)
-    constexpr int NSLAB = D / 32, NT = D / 16;
-    int8_t* kc = static_cast<int8_t*>(const_cast<void*>(a.k_cache));
-    int8_t* vc = static_cast<int8_t*>(const_cast<void*>(a.v_cache));
-    float* kscale = const_cast<float*>(a.k_scale);
-    float* vscale = const_cast<float*>(a.v_scale);
-    const bool fresh = r == 0;  // writing row 0 starts the block afresh
-    const int lane = threadIdx.x & 63;
-    // ---------------- K ----------------
-    {
-        float x[NSLAB][8];
-        float amax = 0.0f;
-#pragma unroll
-        for (int sl = 0; sl < NSLAB; sl++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                x[sl][e] = n == r ? s_new[k_dim0<D>(sl, q4) + e] : 0.0f;
-                const float ax = fabsf(x[sl][e]);
-                amax = ax > amax ? ax : amax;
-            }
-        amax = pa::wave_max(amax);
-        const float old_amax = fresh ? 0.0f : old.k_absmax;
-        const float old_scale = fresh ? 0.0f : old.k_scale;
-        const bool grow = !fresh && amax > old_amax;
-        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
-#pragma unroll
-        for (int sl = 0; sl < NSLAB; sl++) {
-            uint32_t w[2] = {kr[sl].x, kr[sl].y};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                int8_t c;
-                if (n == r) c = pa::quantize_symmetric(x[sl][e], sc);
-                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w[e >> 2], e & 3)) * old_scale, sc);
-                else c = static_cast<int8_t>(code_at(w[e >> 2], e & 3));
-                w[e >> 2] = with_code(w[e >> 2], e & 3, c);
-            }
-            kr[sl] = make_uint2(w[0], w[1]);
-            if (grow || n == r) *reinterpret_cast<uint2*>(kc + tile + n * D + k_dim0<D>(sl, q4)) = kr[sl];
-        }
-        if (lane == 0 && (fresh || grow)) {
-            a.k_absmax[sidx] = amax;
-            kscale[sidx] = sc;
-        }
-        k_scale_out = sc;
-    }
-    // ---------------- V (tile is [D][16]: lane holds tokens 4q4..4q4+3 of dim 16t+n) ----------------
-    {
-        const bool mine = q4 == (r >> 2);
-        const int er = r & 3;
-        float x[NT];
-        float amax = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            x[t] = mine ? s_new[D + 16 * t + n] : 0.0f;
-            const float ax = fabsf(x[t]);
-            amax = ax > amax ? ax : amax;
-        }
-        amax = pa::wave_max(amax);
-        const float old_amax = fresh ? 0.0f : old.v_absmax;
-        const float old_scale = fresh ? 0.0f : old.v_scale;
-        const bool grow = !fresh && amax > old_amax;
-        const float sc = (fresh || grow) ? amax / 127.0f : old_scale;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            uint32_t w = vr[t];
-            int8_t newc = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const bool is_new = mine && e == er;
-                int8_t c;
-                if (is_new) c = newc = pa::quantize_symmetric(x[t], sc);
-                else if (grow) c = pa::quantize_symmetric(static_cast<float>(code_at(w, e)) * old_scale, sc);
-                else c = static_cast<int8_t>(code_at(w, e));
-                w = with_code(w, e, c);
-            }
-            vr[t] = w;
-            int8_t* dst = vc + tile + (16 * t + n) * 16;
-            if (grow) *reinterpret_cast<uint32_t*>(dst + 4 * q4) = w;
-            else if (mine) dst[r] = newc;
-        }
-        if (lane == 0 && (fresh || grow)) {
-            a.v_absmax[sidx] = amax;
-            vscale[sidx] = sc;
-        }
-        v_scale_out = sc;
-    }
-}
-
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferFlags = 0x00020000;
 

@@ -102,14 +102,14 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     // Memory returns in order, so the K/V requests go out first; none of the other values is
     // used right after its load (that would stall the wave on the load's latency).
     float my_ks = 0.0f, my_vs = 0.0f;  // int8: scales of this lane's block
-    // Fused append: the row's last block is entry nbrow - 1 - b0 of the piece that ends the row.
-    // Its wave fetches the new token (lane l: dims l*NPL ..) and, for int8, the block's running
-    // statistics; the token's raw bits (fp32, or bf16 packed two per word) are decoded only at the
-    // patch.
+    // Fused append (bf16 caches; int8 caches are appended by a separate launch first): the row's
+    // last block is entry nbrow - 1 - b0 of the piece that ends the row. Its wave fetches the new
+    // token (lane l: dims l*NPL ..); the token's raw bits (fp32, or bf16 packed two per word) are
+    // decoded only at the patch.
+    static_assert(!(APPEND && KV == PA_DTYPE_INT8), "int8 caches are appended before the decode");
     constexpr int NW = QF32 ? NPL : (NPL + 1) / 2;
     int j_app = -1;
     uint32_t nk_raw[NW], nv_raw[NW];
-    Int8Stats old{};
     if constexpr (APPEND) {
         if (g.b1 == nbrow) j_app = nbrow - 1 - g.b0;  // always the piece's last block
     }
@@ -172,11 +172,6 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                         nv_raw[w] = static_cast<const uint32_t*>(a.v_new)[(src >> 1) + w];
                     }
                 }
-                if constexpr (KV == PA_DTYPE_INT8) {
-                    const int bid = __builtin_amdgcn_readlane(my_bid, j_app);  // list entry j_app
-                    const int64_t sidx = static_cast<int64_t>(bid >= 0 && bid < a.num_blocks ? bid : 0) * Hkv + kvh;
-                    old = Int8Stats{a.k_absmax[sidx], a.k_scale[sidx], a.v_absmax[sidx], a.v_scale[sidx]};
-                }
             }
         }
     };
@@ -218,7 +213,8 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     float& l_run = st.l_run;
     f32x4_t(&acc)[NT] = st.acc;
 
-    auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
+    // app: this call may hold the appended block (only the one outside the loop below does).
+    auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j, bool app) {
         const int e = entry(j);
         const int bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, e));
         float ks = 1.0f, vfac = 1.0f;
@@ -227,7 +223,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             vfac = bid >= 0 ? readlane_f(my_vs, e) : 0.0f;
         }
         if constexpr (APPEND) {
-            if (e == j_app && bid >= 0) {
+            if (app && e == j_app && bid >= 0) {
                 // Stage the new token in this wave's LDS area, then patch the tile.
                 // The empty asm keeps the decoding here: hoisted out of the loop, it would wait
                 // for the token's loads before the first block.
@@ -247,11 +243,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                 __builtin_amdgcn_wave_barrier();
                 const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * TILE;
                 const int r = (T - 1) & 15;
-                if constexpr (KV == PA_DTYPE_INT8)
-                    append_int8_regs<D>(a, tile, static_cast<int64_t>(bid) * Hkv + kvh, s_new, r, q4, n, old, kr,
-                                        vr, ks, vfac);
-                else
-                    append_bf16_regs<D>(a, tile, s_new, r, q4, n, kr, vr);
+                append_bf16_regs<D>(a, tile, s_new, r, q4, n, kr, vr);
             }
         }
         // S^T[token 4q4+i][head n]
@@ -318,19 +310,38 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
         VR va[NT], vb[NT], vx[NT];
         int j = 0;
-        load(ka, va, 0);
-        load(kb, vb, 1);
-        prefetch_next();
-        side_loads();
+        bool peeled = false;
+        if constexpr (APPEND) {
+            if (j_app >= 0) {
+                // Iteration 0 (the appended block) is computed here, outside the loop: with the
+                // patch inlined in the loop body the int8 loop no longer fits the instruction cache
+                // and every wave slows down. The loop then starts at iteration 1 with the same
+                // buffer roles as usual.
+                load(kx, vx, 0);
+                load(ka, va, 1);
+                load(kb, vb, 2);
+                prefetch_next();
+                side_loads();
+                compute(kx, vx, 0, true);
+                j = 1;
+                peeled = true;
+            }
+        }
+        if (!peeled) {
+            load(ka, va, 0);
+            load(kb, vb, 1);
+            prefetch_next();
+            side_loads();
+        }
         while (j < nb) {
             load(kx, vx, j + 2);
-            compute(ka, va, j);
+            compute(ka, va, j, false);
             if (++j >= nb) break;
             load(ka, va, j + 2);
-            compute(kb, vb, j);
+            compute(kb, vb, j, false);
             if (++j >= nb) break;
             load(kb, vb, j + 2);
-            compute(kx, vx, j);
+            compute(kx, vx, j, false);
             ++j;
         }
     }

@@ -37,9 +37,9 @@ void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool appen
     if (kv_dtype == PA_DTYPE_BF16) {
         if (q_f32) pick_append<PA_DTYPE_BF16, true>(a, append, num_seqs, max_grid, s);
         else pick_append<PA_DTYPE_BF16, false>(a, append, num_seqs, max_grid, s);
-    } else {
-        if (q_f32) pick_append<PA_DTYPE_INT8, true>(a, append, num_seqs, max_grid, s);
-        else pick_append<PA_DTYPE_INT8, false>(a, append, num_seqs, max_grid, s);
+    } else {  // int8 caches are appended by a separate launch before the decode
+        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false>(a, num_seqs, max_grid, s);
+        else launch_one<256, PA_DTYPE_INT8, false, false>(a, num_seqs, max_grid, s);
     }
 }
 

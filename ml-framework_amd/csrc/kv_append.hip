@@ -8,6 +8,7 @@
 // int8 one also owns the per-(block, KV head) scale and running absmax.
 #include <string>
 
+#include "append_int8.h"
 #include "pa_internal.h"
 
 namespace {
@@ -31,10 +32,6 @@ __global__ __launch_bounds__(256) void slot_mapping_kernel(
         }
         slot_mapping[dst0 + j] = slot;
     }
-}
-
-__device__ __forceinline__ float load_act(const void* p, bool bf16, int64_t i) {
-    return bf16 ? pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
 // fp32 / bf16 caches: one workgroup per token, blockIdx.y selects K (0) or V (1). K rows are
@@ -79,7 +76,7 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
                 const int h = idx / head_dim, d = idx - h * head_dim;
                 float x[4];
 #pragma unroll
-                for (int k = 0; k < 4; k++) x[k] = load_act(src, in_bf16, (tok0 + 4 * q + k) * n + idx);
+                for (int k = 0; k < 4; k++) x[k] = pa::load_act(src, in_bf16, (tok0 + 4 * q + k) * n + idx);
                 const int64_t row = ((blk * num_kv_heads + h) * head_dim + d) * pa::kBlockSize;  // V row d of the tile
                 if (cache_bf16) {
                     const uint32_t w0 = static_cast<uint32_t>(pa::bf16_trunc(x[0])) | (static_cast<uint32_t>(pa::bf16_trunc(x[1])) << 16);
@@ -94,7 +91,7 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
     }
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         const int h = idx / head_dim, d = idx - h * head_dim;
-        const float x = load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
+        const float x = pa::load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
         const int64_t tile = (blk * num_kv_heads + h) * pa::kBlockSize * head_dim;
         // K tiles are [16][D] (token rows); V tiles are [D][16] (dim rows).
         const int64_t o = is_v ? tile + static_cast<int64_t>(d) * pa::kBlockSize + off : tile + off * head_dim + d;
@@ -103,98 +100,18 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
     }
 }
 
-// int8 caches: one wave per (token, KV head, K|V). Only the wave of the first token of a run of
-// consecutive tokens that land in the same block (a "segment") does work; it owns that
-// (block, head) for the call, so no two waves touch one block's codes or scale.
+// int8 caches: one wave per (token, KV head, K|V); the segment logic is append_int8_segment.
 template <int D>
 __global__ __launch_bounds__(64) void append_int8_kernel(
     const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
     const int64_t* __restrict__ slot_mapping, int32_t n_tok, int8_t* __restrict__ k_cache,
     int8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
     float* __restrict__ k_absmax, float* __restrict__ v_absmax, int32_t num_kv_heads, int64_t capacity) {
-#pragma clang fp contract(off)
-    constexpr int kPer = D / 64;  // elements per lane
-    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const bool is_v = blockIdx.z != 0;
-    const void* src = is_v ? v_new : k_new;
-    int8_t* cache = is_v ? v_cache : k_cache;
-    float* scale = is_v ? v_scale : k_scale;
-    float* absmax = is_v ? v_absmax : k_absmax;
-
-    const int64_t slot = slot_mapping[i];
-    if (slot < 0 || slot >= capacity) return;
-    const int64_t blk = slot / pa::kBlockSize;
-    if (i > 0) {
-        const int64_t prev = slot_mapping[i - 1];
-        if (prev >= 0 && prev < capacity && prev / pa::kBlockSize == blk) return;  // not a segment head
-    }
-    // Extent of the segment, the slots it writes and the absmax of its values for head h.
-    int end = i;
-    uint32_t written = 0;
-    bool fresh = false;
-    float seg_amax = 0.0f;
-    while (end < n_tok) {
-        const int64_t s = slot_mapping[end];
-        if (s < 0 || s >= capacity || s / pa::kBlockSize != blk) break;
-        const int off = static_cast<int>(s % pa::kBlockSize);
-        written |= 1u << off;
-        fresh |= off == 0;
-        const int64_t base = (static_cast<int64_t>(end) * num_kv_heads + h) * D;
-#pragma unroll
-        for (int k = 0; k < kPer; k++) {
-            const float a = fabsf(load_act(src, in_bf16, base + lane + 64 * k));
-            seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
-        }
-        end++;
-    }
-    seg_amax = pa::wave_max(seg_amax);
-
-    const int64_t sidx = blk * num_kv_heads + h;
-    int8_t* block_codes = cache + ((blk * num_kv_heads + h) * pa::kBlockSize) * D;
-    // Element (row off, dim d) of the tile: K is [16][D], V is [D][16].
-    auto at = [&](int off, int d) -> int8_t* {
-        return is_v ? block_codes + d * pa::kBlockSize + off : block_codes + off * D + d;
-    };
-    float cur_scale;
-    if (fresh) {
-        // Writing row 0 starts the block: earlier contents and statistics are discarded.
-        cur_scale = seg_amax / 127.0f;
-        if (lane == 0) {
-            absmax[sidx] = seg_amax;
-            scale[sidx] = cur_scale;
-        }
-    } else {
-        const float old_amax = absmax[sidx];
-        const float old_scale = scale[sidx];
-        cur_scale = old_scale;
-        if (seg_amax > old_amax) {
-            cur_scale = seg_amax / 127.0f;
-            // Requantise every row this segment does not overwrite:
-            // QuantizeSymmetric(Dequantize(q, old_scale), new_scale).
-            for (int off = 0; off < pa::kBlockSize; off++) {
-                if (written & (1u << off)) continue;
-#pragma unroll
-                for (int k = 0; k < kPer; k++) {
-                    int8_t* c = at(off, lane + 64 * k);
-                    const float deq = static_cast<float>(static_cast<int32_t>(*c)) * old_scale;
-                    *c = pa::quantize_symmetric(deq, cur_scale);
-                }
-            }
-            if (lane == 0) {
-                absmax[sidx] = seg_amax;
-                scale[sidx] = cur_scale;
-            }
-        }
-    }
-    for (int t = i; t < end; t++) {
-        const int off = static_cast<int>(slot_mapping[t] % pa::kBlockSize);
-        const int64_t base = (static_cast<int64_t>(t) * num_kv_heads + h) * D;
-#pragma unroll
-        for (int k = 0; k < kPer; k++) {
-            const float x = load_act(src, in_bf16, base + lane + 64 * k);
-            *at(off, lane + 64 * k) = pa::quantize_symmetric(x, cur_scale);
-        }
-    }
+    pa::append_int8_segment<D>(is_v ? v_new : k_new, in_bf16, [&](int t) { return slot_mapping[t]; },
+                               static_cast<int32_t>(blockIdx.x), n_tok, is_v ? v_cache : k_cache,
+                               is_v ? v_scale : k_scale, is_v ? v_absmax : k_absmax,
+                               static_cast<int>(blockIdx.y), num_kv_heads, capacity, is_v);
 }
 
 }  // namespace

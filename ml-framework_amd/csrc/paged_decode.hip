@@ -16,6 +16,7 @@
 // merge over fixed 256/512-token partitions (paged_decode_merge_kernel).
 #include <string>
 
+#include "append_int8.h"
 #include "decode_common.h"
 
 namespace pa {
@@ -115,6 +116,40 @@ __global__ __launch_bounds__(256) void append_last_token_fp32_kernel(const Decod
         kc[tile + r * head_dim + d] = act_at(a.k_new, f32, src);
         vc[tile + d * 16 + r] = act_at(a.v_new, f32, src);
     }
+}
+
+// int8 caches, pa_paged_decode_append: the new token of every sequence (position T - 1, T the
+// clamped context length) is appended by the quantising append of pa_kv_append, as token i = seq
+// i of one call, before the decode reads the cache. One wave per (sequence, KV head, K|V). (Done
+// inside the decode kernel instead, the requantisation stalls the wave that owns each row's last
+// block mid-stream; a separate launch costs less.)
+template <int D>
+__global__ __launch_bounds__(64) void append_last_token_int8_kernel(const DecodeArgs a, int32_t num_seqs) {
+    const bool is_v = blockIdx.z != 0;
+    const int i = static_cast<int>(blockIdx.x), lane = static_cast<int>(threadIdx.x);
+    const int64_t capacity = static_cast<int64_t>(a.num_blocks) * pa::kBlockSize;
+    auto last_slot = [&](int t) -> int64_t {
+        const int T = clamp_len(a, a.context_lens[t]);
+        if (T <= 0) return -1;
+        const int32_t bid = a.block_tables[static_cast<int64_t>(t) * a.max_blocks_per_seq + (T - 1) / pa::kBlockSize];
+        return bid >= 0 ? static_cast<int64_t>(bid) * pa::kBlockSize + (T - 1) % pa::kBlockSize : -1;
+    };
+    // The slots of tokens i - 1 .. i + 62, one per lane, looked up together (a segment rarely spans
+    // more than one token here, and each lookup is two dependent loads).
+    const int t_l = i - 1 + lane;
+    const int64_t my_slot = t_l >= 0 && t_l < num_seqs ? last_slot(t_l) : -1;
+    auto slot_at = [&](int t) -> int64_t {
+        const int k = t - i + 1;
+        if (k < 0 || k >= 64) return last_slot(t);
+        const uint64_t u = static_cast<uint64_t>(my_slot);
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), k);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), k);
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    pa::append_int8_segment<D>(is_v ? a.v_new : a.k_new, a.q_bf16 != 0, slot_at, i,
+                               num_seqs, static_cast<int8_t*>(const_cast<void*>(is_v ? a.v_cache : a.k_cache)),
+                               const_cast<float*>(is_v ? a.v_scale : a.k_scale), is_v ? a.v_absmax : a.k_absmax,
+                               static_cast<int>(blockIdx.y), a.num_kv_heads, capacity, is_v);
 }
 
 }  // namespace
@@ -229,6 +264,16 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     }
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     const int64_t max_grid = max_units > 0 ? max_units : 1;
+    if (append && cfg->kv_dtype == PA_DTYPE_INT8 && num_seqs > 0) {
+        dim3 agrid(num_seqs, cfg->num_kv_heads, 2);
+        switch (cfg->head_dim) {
+            case 64: append_last_token_int8_kernel<64><<<agrid, 64, 0, s>>>(a, num_seqs); break;
+            case 128: append_last_token_int8_kernel<128><<<agrid, 64, 0, s>>>(a, num_seqs); break;
+            default: append_last_token_int8_kernel<256><<<agrid, 64, 0, s>>>(a, num_seqs); break;
+        }
+        PA_HIP_CHECK(hipGetLastError());
+        append = false;  // the decode below reads the appended cache
+    }
     switch (cfg->head_dim) {
         case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
         case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
