@@ -13,7 +13,8 @@ Output: one JSON line. `value` is the achieved algorithmic HBM bandwidth of the 
 tokens/s per layer and us per layer-step ride along. `roofline` covers the same call. `extra`
 times the other configurations the same way: C4 (int8 KV, fused append + decode), C5 (long
 contexts with a shared prefix, decode), C3 (mixed: fused decode of 48 sequences, the append of
-8 prefill chunks and their chunked prefill, with the prefill's MFMA rate). `cpu_baseline` times
+8 prefill chunks and their chunked prefill, with the prefill's MFMA rate) and the whole-block
+moves (copy-on-write copies and swap-out of 4096 blocks, HBM GB/s). `cpu_baseline` times
 the CPU oracle (a C restatement of the reference's StandardPagedAttentionKernel with its
 per-sequence decode loop) on a bounded sample of the C2 batch, on this host.
 """
@@ -313,6 +314,31 @@ def load_traffic():
         return None, None
 
 
+def run_block_moves(timer, stream, steps, warmup, seed):
+    """Copy-on-write (pa_copy_blocks) and swap-out (pa_gather_blocks into a device buffer) of 4096
+    blocks of a C2-shaped bf16 cache (Hkv 8, D 128: 64 KiB of K and V per block); bytes are read +
+    written, 512 MB per call, twice the 256 MB last-level cache, so the rate is HBM's."""
+    import torch
+
+    nb, pairs_n = 16384, 4096
+    cfg = pa.make_config(num_q_heads=32, num_kv_heads=8, head_dim=128, kv_dtype=1, q_dtype=1, num_blocks=nb)
+    kc = torch.zeros((nb, 8, 16, 128), dtype=torch.int16, device="cuda:0")
+    vc = torch.zeros_like(kc)
+    perm = np.random.default_rng(seed).permutation(nb).astype(np.int32)
+    pairs = torch.tensor(np.stack([perm[:pairs_n], perm[pairs_n:2 * pairs_n]], 1), device="cuda:0")
+    ids = torch.tensor(perm[:pairs_n], device="cuda:0")
+    rec = pa.block_bytes(cfg)
+    packed = torch.empty((pairs_n, rec), dtype=torch.uint8, device="cuda:0")
+    ms_copy = timer(lambda: pa.copy_blocks(stream, cfg, kc, vc, None, None, None, None, pairs, pairs_n), steps, warmup)
+    ms_gather = timer(lambda: pa.gather_blocks(stream, cfg, kc, vc, None, None, None, None, ids, pairs_n, packed),
+                      steps, warmup)
+    moved = 2 * pairs_n * rec  # bytes read + written
+    return {"blocks": pairs_n, "bytes_per_block": rec,
+            "copy_blocks_us": round(ms_copy * 1e3, 2), "copy_blocks_gbps": round(moved / (ms_copy * 1e-3) / 1e9, 1),
+            "gather_blocks_us": round(ms_gather * 1e3, 2),
+            "gather_blocks_gbps": round(moved / (ms_gather * 1e-3) / 1e9, 1)}
+
+
 GRAPH_CALLS = 32  # layer-steps per captured graph: one decode step of a 32-layer (Llama-3-8B) model
 
 
@@ -413,6 +439,8 @@ def main():
             log(f"[bench] C5 {c5['us_per_layer_step']} us")
             extra["C3"] = run_c3(timer, stream, n, args.warmup, 3)
             log(f"[bench] C3 {extra['C3']['us_per_layer_step']} us")
+            extra["block_moves"] = run_block_moves(timer, stream, n, args.warmup, 4)
+            log(f"[bench] block moves {extra['block_moves']}")
             torch.cuda.empty_cache()
     torch.cuda.synchronize()
     if args.copy_calibration_mb > 0:

@@ -266,6 +266,50 @@ pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out
                              const int32_t* block_tables, int32_t num_seqs,
                              int32_t max_blocks_per_seq, int32_t max_chunk_len);
 
+/* ---- whole-block moves: copy-on-write and swap (the copy the reference leaves to a comment at
+ *      beam divergence, BeamSearchBlockSharing.OnBeamDivergence, Sharing/BeamSearchBlockSharing.cs:
+ *      69-79, over the refcounts of BlockShareManager.cs:34-105; and the block data moves of
+ *      IPagedAttentionCache.GetBlockData / StoreBlockData, ContinuousBatching/KVCache/
+ *      IPagedAttentionCache.cs:40-47, CacheBlockData.cs:7-12, which has no implementation) ----
+ * Cache pointers (and the packed buffer) must be 16-byte aligned. int8 caches carry their
+ * per-(block, KV head) k_scale, v_scale, k_absmax, v_absmax with the codes. */
+
+/* Bytes of one packed block record: K of all KV heads (num_kv_heads * 16 * head_dim elements),
+ * then V (same), then for int8 k_scale[Hkv], v_scale[Hkv], k_absmax[Hkv], v_absmax[Hkv] (fp32).
+ * A multiple of 16. */
+pa_status pa_block_bytes(const pa_config* cfg, size_t* bytes);
+/* Copy-on-write: block_pairs [num_pairs][2] int32 (device) = (src, dst); every KV head's K and V
+ * tiles (and int8 statistics) of block src are copied into block dst. Pairs with an id outside
+ * [0, num_blocks) or src == dst are skipped. Within one call no block may be written twice, nor
+ * be both a source and a destination. */
+pa_status pa_copy_blocks(pa_stream* stream, const pa_config* cfg, void* k_cache, void* v_cache,
+                         float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
+                         const int32_t* block_pairs, int32_t num_pairs);
+/* Swap-out: record i of `packed` ([n] records of pa_block_bytes, device memory; pa_memcpy moves
+ * the records to and from host memory) receives block block_ids[i] (device int32), bit for bit.
+ * Ids outside [0, num_blocks) are skipped (their records are not written). */
+pa_status pa_gather_blocks(pa_stream* stream, const pa_config* cfg, const void* k_cache, const void* v_cache,
+                           const float* k_scale, const float* v_scale, const float* k_absmax,
+                           const float* v_absmax, const int32_t* block_ids, int32_t n, void* packed);
+/* Swap-in: block block_ids[i] receives record i of `packed`, bit for bit (ids outside
+ * [0, num_blocks) skipped; no block twice in one call). */
+pa_status pa_scatter_blocks(pa_stream* stream, const pa_config* cfg, void* k_cache, void* v_cache,
+                            float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
+                            const int32_t* block_ids, int32_t n, const void* packed);
+/* GetBlockData: tokens [0, tokens) (tokens <= 16) of block `block` as fp32, k_out / v_out
+ * [tokens][num_kv_heads][head_dim] (device memory); bf16 widens exactly, int8 is code * scale.
+ * k_scale/v_scale are needed for int8 only. */
+pa_status pa_read_block_f32(pa_stream* stream, const pa_config* cfg, const void* k_cache, const void* v_cache,
+                            const float* k_scale, const float* v_scale, int32_t block, int32_t tokens,
+                            float* k_out, float* v_out);
+/* StoreBlockData: tokens [0, tokens) of block `block` from fp32 k_in / v_in
+ * [tokens][num_kv_heads][head_dim]; the cache bytes and int8 statistics afterwards are those of
+ * pa_kv_append with fp32 input at slots block * 16 + t (row 0 is written, so an int8 block
+ * starts afresh with scale = absmax of the new rows / 127). */
+pa_status pa_write_block_f32(pa_stream* stream, const pa_config* cfg, void* k_cache, void* v_cache,
+                             float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
+                             int32_t block, int32_t tokens, const float* k_in, const float* v_in);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,8 @@ EXPORTS = (
     "pa_graph_destroy",
     "pa_build_slot_mapping", "pa_kv_append", "pa_decode_workspace_size", "pa_paged_decode",
     "pa_paged_decode_append", "pa_chunked_prefill",
+    "pa_block_bytes", "pa_copy_blocks", "pa_gather_blocks", "pa_scatter_blocks", "pa_read_block_f32",
+    "pa_write_block_f32",
 )
 
 
@@ -138,6 +140,12 @@ _SIGNATURES = {
     "pa_paged_decode_append": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                _P, _SZ],
     "pa_chunked_prefill": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
+    "pa_block_bytes": [_CFG, ctypes.POINTER(_SZ)],
+    "pa_copy_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32],
+    "pa_gather_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32, _P],
+    "pa_scatter_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32, _P],
+    "pa_read_block_f32": [_P, _CFG, _P, _P, _P, _P, _I32, _I32, _P, _P],
+    "pa_write_block_f32": [_P, _CFG, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P],
 }
 
 _lib = None
@@ -332,6 +340,42 @@ def chunked_prefill(stream, cfg: PaConfig, out, q, q_start_loc, prefix_lens, k_c
     call("pa_chunked_prefill", stream.handle if stream else None, ctypes.byref(cfg), _ptr(out),
          _ptr(q), _ptr(q_start_loc), _ptr(prefix_lens), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
          _ptr(v_scale), _ptr(block_tables), num_seqs, max_blocks_per_seq, max_chunk_len)
+
+
+# ---- whole-block moves (copy-on-write, swap) ---------------------------------------------------
+def block_bytes(cfg: PaConfig) -> int:
+    n = ctypes.c_size_t()
+    call("pa_block_bytes", ctypes.byref(cfg), ctypes.byref(n))
+    return n.value
+
+
+def copy_blocks(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, k_absmax, v_absmax, block_pairs,
+                num_pairs):
+    call("pa_copy_blocks", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
+         _ptr(k_scale), _ptr(v_scale), _ptr(k_absmax), _ptr(v_absmax), _ptr(block_pairs), num_pairs)
+
+
+def gather_blocks(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, k_absmax, v_absmax, block_ids, n,
+                  packed):
+    call("pa_gather_blocks", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
+         _ptr(k_scale), _ptr(v_scale), _ptr(k_absmax), _ptr(v_absmax), _ptr(block_ids), n, _ptr(packed))
+
+
+def scatter_blocks(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, k_absmax, v_absmax, block_ids, n,
+                   packed):
+    call("pa_scatter_blocks", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
+         _ptr(k_scale), _ptr(v_scale), _ptr(k_absmax), _ptr(v_absmax), _ptr(block_ids), n, _ptr(packed))
+
+
+def read_block_f32(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, block, tokens, k_out, v_out):
+    call("pa_read_block_f32", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
+         _ptr(k_scale), _ptr(v_scale), block, tokens, _ptr(k_out), _ptr(v_out))
+
+
+def write_block_f32(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, k_absmax, v_absmax, block, tokens,
+                    k_in, v_in):
+    call("pa_write_block_f32", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
+         _ptr(k_scale), _ptr(v_scale), _ptr(k_absmax), _ptr(v_absmax), block, tokens, _ptr(k_in), _ptr(v_in))
 
 
 @dataclass

@@ -164,3 +164,76 @@ def chunked_prefill(cfg, q, q_start_loc, prefix_lens, k_cache, v_cache, k_scale,
                                    _p(v_scale), _p(block_tables), S, block_tables.shape[1], n_threads)
     assert rc == 0
     return out
+
+
+# ---- whole-block moves (numpy: pure data movement) ---------------------------------------------
+# Copy-on-write and swap of paged blocks: the copy the reference leaves to a comment at beam
+# divergence (Sharing/BeamSearchBlockSharing.cs:69-79) and the block data moves of
+# IPagedAttentionCache.GetBlockData / StoreBlockData (ContinuousBatching/KVCache/
+# IPagedAttentionCache.cs:40-47, CacheBlockData.cs:7-12). Caches are numpy arrays whose first axis
+# is the block; the statistics (int8) are [num_blocks][Hkv] float32 arrays, in the order
+# k_scale, v_scale, k_absmax, v_absmax.
+
+def _rows(a, nb):
+    return a.reshape(nb, -1)
+
+
+def copy_blocks(cfg, k_cache, v_cache, stats, pairs):
+    """In place: block dst := block src for each valid pair with src != dst (pa_copy_blocks)."""
+    nb = cfg.num_blocks
+    for src, dst in np.asarray(pairs, np.int64).reshape(-1, 2):
+        if not (0 <= src < nb and 0 <= dst < nb) or src == dst:
+            continue
+        for a in (k_cache, v_cache) + tuple(s for s in (stats or ()) if s is not None):
+            _rows(a, nb)[dst] = _rows(a, nb)[src]
+
+
+def block_record_bytes(cfg):
+    elt = {0: 4, 1: 2, 2: 1}[cfg.kv_dtype]
+    part = cfg.num_kv_heads * 16 * cfg.head_dim * elt
+    return 2 * part + (16 * cfg.num_kv_heads if cfg.kv_dtype == 2 else 0)
+
+
+def gather_blocks(cfg, k_cache, v_cache, stats, block_ids, packed):
+    """Record i of packed (uint8 [n][record]) := K bytes, V bytes, then k_scale, v_scale,
+    k_absmax, v_absmax of block block_ids[i] (pa_gather_blocks); invalid ids leave the record."""
+    nb = cfg.num_blocks
+    for i, b in enumerate(np.asarray(block_ids, np.int64)):
+        if not 0 <= b < nb:
+            continue
+        parts = [_rows(k_cache, nb)[b].view(np.uint8), _rows(v_cache, nb)[b].view(np.uint8)]
+        if cfg.kv_dtype == 2:
+            parts += [np.ascontiguousarray(s[b]).view(np.uint8) for s in stats]
+        packed[i] = np.concatenate(parts)
+
+
+def scatter_blocks(cfg, k_cache, v_cache, stats, block_ids, packed):
+    """Block block_ids[i] := record i of packed (pa_scatter_blocks)."""
+    nb = cfg.num_blocks
+    part = _rows(k_cache, nb)[0].view(np.uint8).size
+    for i, b in enumerate(np.asarray(block_ids, np.int64)):
+        if not 0 <= b < nb:
+            continue
+        rec = packed[i]
+        _rows(k_cache, nb)[b] = rec[:part].view(k_cache.dtype)
+        _rows(v_cache, nb)[b] = rec[part:2 * part].view(v_cache.dtype)
+        if cfg.kv_dtype == 2:
+            hkv = cfg.num_kv_heads
+            for j, s in enumerate(stats):
+                s[b] = rec[2 * part + 4 * hkv * j:2 * part + 4 * hkv * (j + 1)].view(np.float32)
+
+
+def read_block_f32(cfg, k_cache, v_cache, k_scale, v_scale, block, tokens):
+    """Tokens [0, tokens) of a block as fp32 [tokens][Hkv][D] (pa_read_block_f32): K tile
+    [16][D], V tile [D][16]; bf16 widened, int8 code * scale (Dequantize,
+    Quantization/Operations/QuantizationOperations.cs:83-88)."""
+    nb, hkv, d = cfg.num_blocks, cfg.num_kv_heads, cfg.head_dim
+    kt = k_cache.reshape(nb, hkv, 16, d)[block, :, :tokens, :]        # [Hkv][t][D]
+    vt = v_cache.reshape(nb, hkv, d, 16)[block, :, :, :tokens]        # [Hkv][D][t]
+    if cfg.kv_dtype == 1:
+        kt, vt = f32_from_bf16(kt), f32_from_bf16(vt)
+    elif cfg.kv_dtype == 2:
+        kt = kt.astype(np.float32) * k_scale[block][:, None, None]
+        vt = vt.astype(np.float32) * v_scale[block][:, None, None]
+    return (np.ascontiguousarray(np.transpose(kt, (1, 0, 2)).astype(np.float32)),
+            np.ascontiguousarray(np.transpose(vt, (2, 0, 1)).astype(np.float32)))

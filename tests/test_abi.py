@@ -144,3 +144,26 @@ def test_device_open_without_gpu_reports_no_device():
         with pytest.raises(pa.PagedAttentionError) as e:
             pa.Device(0)
         assert e.value.status == pa.PA_ERROR_NO_DEVICE
+
+
+def test_block_moves_validate_on_the_host():
+    c = cfg()  # bf16, Hkv 8, D 128
+    assert pa.block_bytes(c) == 2 * 8 * 16 * 128 * 2
+    assert pa.block_bytes(cfg(kv_dtype=2)) == 2 * 8 * 16 * 128 + 4 * 8 * 4
+    bad = [
+        lambda: pa.read_block_f32(None, c, 4096, 4096, None, None, c.num_blocks, 4, 4096, 4096),  # block
+        lambda: pa.read_block_f32(None, c, 4096, 4096, None, None, 0, 17, 4096, 4096),            # tokens
+        lambda: pa.write_block_f32(None, c, 4096, 4096, None, None, None, None, -1, 4, 4096, 4096),
+        lambda: pa.copy_blocks(None, c, 4100, 4096, None, None, None, None, 4096, 1),              # alignment
+        lambda: pa.copy_blocks(None, c, 4096, 4096, None, None, None, None, None, 1),              # pairs
+        lambda: pa.gather_blocks(None, c, 4096, 4096, None, None, None, None, 4096, 1, 4104),       # packed
+        lambda: pa.scatter_blocks(None, cfg(kv_dtype=2), 4096, 4096, None, None, None, None, 4096, 1, 4096),
+    ]
+    for f in bad:
+        with pytest.raises(pa.PagedAttentionError) as e:
+            f()
+        assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    # empty calls are no-ops that succeed without touching memory
+    pa.copy_blocks(None, c, 4096, 4096, None, None, None, None, None, 0)
+    pa.gather_blocks(None, c, 4096, 4096, None, None, None, None, None, 0, None)
+    pa.read_block_f32(None, c, 4096, 4096, None, None, 0, 0, None, None)
