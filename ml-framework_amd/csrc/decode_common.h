@@ -281,15 +281,21 @@ __device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t ti
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferFlags = 0x00020000;
 
-template <typename T> __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, int off);
-template <> __device__ __forceinline__ uint4 buffer_load<uint4>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-template <> __device__ __forceinline__ uint2 buffer_load<uint2>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-}
-template <> __device__ __forceinline__ uint32_t buffer_load<uint32_t>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+// CP: the load's cache-policy operand; kLoadNonTemporal marks data that is not read again soon.
+// Measured on the decode's K/V stream: int8 caches (C4) 143 -> 132 us with it, bf16 caches
+// slower (C2 66 -> 78 us, and C5, whose shared prefix is re-read from the last-level cache, 127 ->
+// 159 us), so only the int8 decode uses it.
+constexpr int kLoadDefault = 0;
+constexpr int kLoadNonTemporal = 2;
+template <typename T, int CP = kLoadDefault> __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (sizeof(T) == 16) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
+    } else if constexpr (sizeof(T) == 8) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP));
+    } else {
+        static_assert(sizeof(T) == 4, "16-, 8- or 4-byte loads");
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP));
+    }
 }
 
 // ---- launchers (one translation unit per kernel family) ----------------------------------------

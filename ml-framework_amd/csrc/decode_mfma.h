@@ -181,6 +181,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     using KR = typename Raw::K;
     using VR = typename Raw::V;
     const int k_lane_off = (n * D + k_dim0<D>(0, q4)) * ELT;  // K row n, D / 4 dims from here
+    constexpr int kLoadCP = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
     const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
     // Loads go through per-block buffer descriptors: a block past the wave's list or with an
     // invalid id gets a zero-sized descriptor, so its loads return zeros without touching memory.
@@ -197,16 +198,16 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
 #pragma unroll
             for (int s = 0; s < NSLAB; s += 2) {
-                const uint4 w = buffer_load<uint4>(rk, k_lane_off + 8 * s);
+                const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_lane_off + 8 * s);
                 kr[s] = make_uint2(w.x, w.y);
                 kr[s + 1] = make_uint2(w.z, w.w);
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR>(rk, k_lane_off + 8 * s * ELT);
+            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kLoadCP>(rk, k_lane_off + 8 * s * ELT);
         }
 #pragma unroll
-        for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR>(rv, v_lane_off + 256 * t * ELT);
+        for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kLoadCP>(rv, v_lane_off + 256 * t * ELT);
     };
 
     float& m_run = st.m_run;
