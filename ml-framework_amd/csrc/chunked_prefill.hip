@@ -287,14 +287,6 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                     for (int i = 0; i < 4; i++) v[k][4 * h + i] = sacc[i];
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);  // keep the V reads after QK (register pressure)
-            bf16x8_t vop[NT];
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const int d = 16 * t + n;
-                if constexpr (ELT == 2) vop[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1) * 16));
-                else vop[t] = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0) * 16 + (q4 >> 1) * 8));
-            }
             if constexpr (KV == PA_DTYPE_INT8) {
                 const float mult = c2 * s_ksc[jl + pblk];  // 0 for an invalid block
 #pragma unroll
@@ -339,6 +331,11 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                         for (int i = 0; i < 4; i++) acc[k][t][i] *= ar[i];
                 }
             }
+            // P of both units (high and low bf16 parts) first, then each V operand is read from LDS
+            // right before the four MFMAs that use it: holding all NT V operands across the two
+            // units' PV products pushed the kernel past 256 VGPRs into scratch spills, whose
+            // reloads inside the loop wait for every load in flight.
+            bf16x8_t phi[2], plo[2];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 float p[8];
@@ -363,16 +360,26 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                     hi[e] = pack_bf16_trunc(a0, a1);
                     lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
                 }
-                const bf16x8_t phi = __builtin_bit_cast(bf16x8_t, make_uint4(hi[0], hi[1], hi[2], hi[3]));
-                const bf16x8_t plo = __builtin_bit_cast(bf16x8_t, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                phi[k] = __builtin_bit_cast(bf16x8_t, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                plo[k] = __builtin_bit_cast(bf16x8_t, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+            }
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, vop[t], acc[k][t], 0, 0, 0);
-                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, vop[t], acc[k][t], 0, 0, 0);
+            for (int t = 0; t < NT; t++) {
+                const int d = 16 * t + n;
+                bf16x8_t vop;
+                if constexpr (ELT == 2) vop = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1) * 16));
+                else vop = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0) * 16 + (q4 >> 1) * 8));
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[k], vop, acc[k][t], 0, 0, 0);
+                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[k], vop, acc[k][t], 0, 0, 0);
                 }
-                if constexpr (KV != PA_DTYPE_INT8) {
-                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi, ones, acc_l[k], 0, 0, 0);
-                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo, ones, acc_l[k], 0, 0, 0);
+            }
+            if constexpr (KV != PA_DTYPE_INT8) {
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[k], ones, acc_l[k], 0, 0, 0);
+                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[k], ones, acc_l[k], 0, 0, 0);
                 }
             }
         };
