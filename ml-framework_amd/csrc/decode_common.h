@@ -84,8 +84,9 @@ template <> struct MfmaRaw<PA_DTYPE_INT8> {
 };
 
 // fp32 -> bf16 bits by truncation (the reference's conversion, BFloat16.cs:99-107).
+// One v_perm_b32: bytes 3, 2 of hi over bytes 3, 2 of lo, i.e. (hi & 0xffff0000) | (lo >> 16).
 __device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
-    return (__float_as_uint(hi) & 0xffff0000u) | (__float_as_uint(lo) >> 16);
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 __device__ __forceinline__ uint32_t pack_i8pair(uint32_t w, int k) {
