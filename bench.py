@@ -14,7 +14,8 @@ tokens/s per layer and us per layer-step ride along. `roofline` covers the same 
 times the other configurations the same way: C4 (int8 KV, fused append + decode), C5 (long
 contexts with a shared prefix, decode), C3 (mixed: fused decode of 48 sequences, the append of
 8 prefill chunks and their chunked prefill, with the prefill's MFMA rate) and the whole-block
-moves (copy-on-write copies and swap-out of 4096 blocks, HBM GB/s). `cpu_baseline` times
+moves (copy-on-write copies and swap-out of 4096 blocks, HBM GB/s) and a whole C2 decode layer
+with its Q/K/V and output projections (Llama-3-8B weights). `cpu_baseline` times
 the CPU oracle (a C restatement of the reference's StandardPagedAttentionKernel with its
 per-sequence decode loop) on a bounded sample of the C2 batch, on this host.
 """
@@ -339,6 +340,57 @@ def run_block_moves(timer, stream, steps, warmup, seed):
             "gather_blocks_gbps": round(moved / (ms_gather * 1e-3) / 1e9, 1)}
 
 
+def run_layer(timer, stream, w, inp, steps, warmup, seed):
+    """One whole decode layer of the C2 batch with Llama-3-8B projection weights (hidden 4096,
+    bf16): pa_qkv_project_append (x . W_qkv^T, Q out, K/V appended), pa_paged_decode over the
+    cache, pa_o_project. Times each call and the three in sequence; the GEMMs are weight-bound, so
+    their rate is weight bytes per second."""
+    import torch
+
+    hidden, S = 4096, w.num_seqs
+    cfg = config_of(w, 0)
+    hq, hkv, d = w.num_q_heads, w.num_kv_heads, w.head_dim
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(seed)
+    bf = lambda *shape: (torch.randn(*shape, generator=g, device="cuda:0") * 0.02).to(torch.bfloat16)
+    x = bf(S, hidden)
+    w_qkv = bf((hq + 2 * hkv) * d, hidden)
+    w_o = bf(hidden, hq * d)
+    q = torch.empty((S, hq, d), dtype=torch.bfloat16, device="cuda:0")
+    attn = torch.empty((S, hq, d), dtype=torch.float32, device="cuda:0")
+    y = torch.empty((S, hidden), dtype=torch.float32, device="cuda:0")
+    qws_b, ows_b = pa.qkv_workspace_size(cfg, S), pa.o_workspace_size(cfg, S)
+    qws = torch.empty(qws_b, dtype=torch.uint8, device="cuda:0")
+    ows = torch.empty(ows_b, dtype=torch.uint8, device="cuda:0")
+    dws_b = pa.decode_workspace_size(cfg, S, w.max_context_len)
+    dws = torch.empty(max(dws_b, 1), dtype=torch.uint8, device="cuda:0")
+    pos = w.context_lens.astype(np.int64) - 1
+    slots = tensor(w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16)
+
+    def qkv():
+        pa.qkv_project_append(stream, cfg, x, w_qkv, hidden, S, slots, q, inp["k_cache"], inp["v_cache"], None, None,
+                              None, None, qws, qws_b)
+
+    def dec():
+        pa.paged_decode(stream, cfg, attn, q, inp["k_cache"], inp["v_cache"], None, None, inp["tables"], inp["lens"],
+                        S, w.max_blocks, w.max_context_len, dws, dws_b)
+
+    def oproj():
+        pa.o_project(stream, cfg, attn, w_o, hidden, S, y, ows, ows_b)
+
+    def layer():
+        qkv(); dec(); oproj()
+
+    qkv()  # creates the device's rocBLAS handle outside the timed region
+    stream.synchronize()
+    t = {k: timer(f, steps, warmup) * 1e3 for k, f in (("qkv", qkv), ("decode", dec), ("o", oproj), ("layer", layer))}
+    wq_bytes, wo_bytes = w_qkv.numel() * 2, w_o.numel() * 2
+    return {"hidden": hidden, "qkv_project_append_us": round(t["qkv"], 2),
+            "qkv_weight_gbps": round(wq_bytes / (t["qkv"] * 1e-6) / 1e9, 1),
+            "decode_us": round(t["decode"], 2), "o_project_us": round(t["o"], 2),
+            "o_weight_gbps": round(wo_bytes / (t["o"] * 1e-6) / 1e9, 1), "layer_us": round(t["layer"], 2)}
+
+
 GRAPH_CALLS = 32  # layer-steps per captured graph: one decode step of a 32-layer (Llama-3-8B) model
 
 
@@ -441,6 +493,8 @@ def main():
             log(f"[bench] C3 {extra['C3']['us_per_layer_step']} us")
             extra["block_moves"] = run_block_moves(timer, stream, n, args.warmup, 4)
             log(f"[bench] block moves {extra['block_moves']}")
+            extra["C2_layer"] = run_layer(timer, stream, w, inp, n, args.warmup, 5)
+            log(f"[bench] C2 layer with projections {extra['C2_layer']}")
             torch.cuda.empty_cache()
     torch.cuda.synchronize()
     if args.copy_calibration_mb > 0:

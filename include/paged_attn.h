@@ -310,6 +310,31 @@ pa_status pa_write_block_f32(pa_stream* stream, const pa_config* cfg, void* k_ca
                              float* k_scale, float* v_scale, float* k_absmax, float* v_absmax,
                              int32_t block, int32_t tokens, const float* k_in, const float* v_in);
 
+/* ---- the projections either side of attention (PagedAttentionLayer.ComputeAttention's
+ *      _queryProj/_keyProj/_valueProj.Forward + UpdateKVCache and _outputProj.Forward,
+ *      Layers/PagedAttentionLayer.cs:112-142; Linear.Forward y = x W^T without bias,
+ *      Modules/Linear.cs:81-110). bf16 weights and activations (cfg->q_dtype must be BF16), fp32
+ *      accumulation; the GEMMs run on rocBLAS. The first call on a device creates its rocBLAS
+ *      handle, so make one call before capturing these into a graph. ---- */
+
+/* Bytes of workspace pa_qkv_project_append needs for n_tok tokens: the fp32 GEMM output
+ * [n_tok][(num_q_heads + 2 num_kv_heads) head_dim]. */
+pa_status pa_qkv_workspace_size(const pa_config* cfg, int32_t n_tok, size_t* bytes);
+/* x [n_tok][hidden] bf16; w_qkv [(Hq + 2 Hkv) * head_dim][hidden] bf16, the rows of Wq, then Wk,
+ * then Wv. y = x w_qkv^T (fp32); q_out [n_tok][Hq][head_dim] (bf16) = y's Q columns truncated; the
+ * K and V columns are appended into the cache at slot_mapping exactly as pa_kv_append does with
+ * fp32 input (the int8 statistics included). */
+pa_status pa_qkv_project_append(pa_stream* stream, const pa_config* cfg, const void* x, const void* w_qkv,
+                                int32_t hidden, int32_t n_tok, const int64_t* slot_mapping, void* q_out,
+                                void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                                float* k_absmax, float* v_absmax, void* workspace, size_t workspace_bytes);
+/* Bytes of workspace pa_o_project needs for n_tok tokens (a bf16 copy of the attention output). */
+pa_status pa_o_workspace_size(const pa_config* cfg, int32_t n_tok, size_t* bytes);
+/* attn [n_tok][Hq][head_dim] fp32 (the decode / prefill output), truncated to bf16;
+ * w_o [hidden][Hq * head_dim] bf16; y [n_tok][hidden] fp32 = attn_bf16 w_o^T. */
+pa_status pa_o_project(pa_stream* stream, const pa_config* cfg, const float* attn, const void* w_o,
+                       int32_t hidden, int32_t n_tok, float* y, void* workspace, size_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,10 +19,12 @@ __device__ __forceinline__ float load_act(const void* p, bool bf16, int64_t i) {
 }
 
 // Wave (64 lanes) for token i of the call, KV head h, K (is_v false) or V. slot_at(t) is the slot
-// of token t (out of [0, capacity): skipped); src holds the tokens' values, [n_tok][num_kv_heads][D]
-// in the activation dtype. The tile of (block, h) is K [16][D] or V [D][16] in `cache`.
+// of token t (out of [0, capacity): skipped); src holds the tokens' values in the activation dtype,
+// token t's (head h, dim d) at t * tok_stride + h * D + d. The tile of (block, h) is K [16][D] or
+// V [D][16] in `cache`.
 template <int D, typename SlotAt>
-__device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf16, SlotAt slot_at, int32_t i,
+__device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf16, int64_t tok_stride, SlotAt slot_at,
+                                                    int32_t i,
                                                     int32_t n_tok, int8_t* cache, float* scale, float* absmax,
                                                     int h, int32_t num_kv_heads, int64_t capacity, bool is_v) {
 #pragma clang fp contract(off)
@@ -46,7 +48,7 @@ __device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf1
         const int off = static_cast<int>(s % kBlockSize);
         written |= 1u << off;
         fresh |= off == 0;
-        const int64_t base = (static_cast<int64_t>(end) * num_kv_heads + h) * D;
+        const int64_t base = static_cast<int64_t>(end) * tok_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
         for (int k = 0; k < kPer; k++) {
             const float a = fabsf(load_act(src, in_bf16, base + lane + 64 * k));
@@ -95,7 +97,7 @@ __device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf1
     }
     for (int t = i; t < end; t++) {
         const int off = static_cast<int>(slot_at(t) % kBlockSize);
-        const int64_t base = (static_cast<int64_t>(t) * num_kv_heads + h) * D;
+        const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
         for (int k = 0; k < kPer; k++) {
             const float x = load_act(src, in_bf16, base + lane + 64 * k);

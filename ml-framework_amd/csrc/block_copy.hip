@@ -150,7 +150,7 @@ __global__ __launch_bounds__(64) void write_block_int8_kernel(CacheRefs c, int32
     const bool is_v = blockIdx.y != 0;
     const int64_t capacity = static_cast<int64_t>(c.num_blocks) * pa::kBlockSize;
     pa::append_int8_segment<D>(is_v ? static_cast<const void*>(v_in) : static_cast<const void*>(k_in), false,
-                               [&](int t) { return static_cast<int64_t>(block) * pa::kBlockSize + t; }, 0, tokens,
+                               static_cast<int64_t>(c.hkv) * D, [&](int t) { return static_cast<int64_t>(block) * pa::kBlockSize + t; }, 0, tokens,
                                reinterpret_cast<int8_t*>(is_v ? c.v : c.k), c.stat[is_v ? 1 : 0],
                                c.stat[is_v ? 3 : 2], static_cast<int>(blockIdx.x), c.hkv, capacity, is_v);
 }

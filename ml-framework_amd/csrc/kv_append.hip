@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void slot_mapping_kernel(
 __global__ __launch_bounds__(256) void append_plain_kernel(
     const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
     const int64_t* __restrict__ slot_mapping, int32_t n_tok, void* __restrict__ k_cache, void* __restrict__ v_cache,
-    bool cache_bf16, int32_t num_kv_heads, int32_t head_dim, int64_t capacity) {
+    bool cache_bf16, int32_t num_kv_heads, int32_t head_dim, int64_t capacity, int64_t tok_stride) {
+    // Token t's values for (head h, dim d) are at t * tok_stride + h * head_dim + d of k_new / v_new.
     const int i = blockIdx.x;
     const int64_t slot = slot_mapping[i];
     if (slot < 0 || slot >= capacity) return;
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
                 const int h = idx / head_dim, d = idx - h * head_dim;
                 float x[4];
 #pragma unroll
-                for (int k = 0; k < 4; k++) x[k] = pa::load_act(src, in_bf16, (tok0 + 4 * q + k) * n + idx);
+                for (int k = 0; k < 4; k++) x[k] = pa::load_act(src, in_bf16, (tok0 + 4 * q + k) * tok_stride + idx);
                 const int64_t row = ((blk * num_kv_heads + h) * head_dim + d) * pa::kBlockSize;  // V row d of the tile
                 if (cache_bf16) {
                     const uint32_t w0 = static_cast<uint32_t>(pa::bf16_trunc(x[0])) | (static_cast<uint32_t>(pa::bf16_trunc(x[1])) << 16);
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
     }
     for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
         const int h = idx / head_dim, d = idx - h * head_dim;
-        const float x = pa::load_act(src, in_bf16, static_cast<int64_t>(i) * n + idx);
+        const float x = pa::load_act(src, in_bf16, static_cast<int64_t>(i) * tok_stride + idx);
         const int64_t tile = (blk * num_kv_heads + h) * pa::kBlockSize * head_dim;
         // K tiles are [16][D] (token rows); V tiles are [D][16] (dim rows).
         const int64_t o = is_v ? tile + static_cast<int64_t>(d) * pa::kBlockSize + off : tile + off * head_dim + d;
@@ -106,9 +107,10 @@ __global__ __launch_bounds__(64) void append_int8_kernel(
     const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
     const int64_t* __restrict__ slot_mapping, int32_t n_tok, int8_t* __restrict__ k_cache,
     int8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
-    float* __restrict__ k_absmax, float* __restrict__ v_absmax, int32_t num_kv_heads, int64_t capacity) {
+    float* __restrict__ k_absmax, float* __restrict__ v_absmax, int32_t num_kv_heads, int64_t capacity,
+    int64_t tok_stride) {
     const bool is_v = blockIdx.z != 0;
-    pa::append_int8_segment<D>(is_v ? v_new : k_new, in_bf16, [&](int t) { return slot_mapping[t]; },
+    pa::append_int8_segment<D>(is_v ? v_new : k_new, in_bf16, tok_stride, [&](int t) { return slot_mapping[t]; },
                                static_cast<int32_t>(blockIdx.x), n_tok, is_v ? v_cache : k_cache,
                                is_v ? v_scale : k_scale, is_v ? v_absmax : k_absmax,
                                static_cast<int>(blockIdx.y), num_kv_heads, capacity, is_v);
@@ -140,52 +142,66 @@ pa_status pa_build_slot_mapping(pa_stream* stream, const pa_config* cfg,
     PA_HIP_CHECK(hipGetLastError());
     return pa::clear_error();
 }
+}  // extern "C"
+
+namespace pa {
+
+pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, const void* k_new, const void* v_new,
+                           bool in_bf16, int64_t tok_stride, const int64_t* slot_mapping, int32_t n_tok,
+                           void* k_cache, void* v_cache, float* k_scale, float* v_scale, float* k_absmax,
+                           float* v_absmax) {
+    const std::string fn(f);
+    if (n_tok < 0) return set_error(PA_ERROR_INVALID_ARGUMENT, fn + ": n_tok < 0");
+    if (n_tok == 0) return clear_error();
+    if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache)
+        return set_error(PA_ERROR_INVALID_ARGUMENT, fn + ": null pointer");
+    const int64_t capacity = static_cast<int64_t>(cfg->num_blocks) * kBlockSize;
+    if (cfg->kv_dtype != PA_DTYPE_INT8) {
+        dim3 grid(n_tok, 2);
+        append_plain_kernel<<<grid, 256, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, k_cache, v_cache,
+                                                  cfg->kv_dtype == PA_DTYPE_BF16, cfg->num_kv_heads, cfg->head_dim,
+                                                  capacity, tok_stride);
+    } else {
+        if (!k_scale || !v_scale || !k_absmax || !v_absmax)
+            return set_error(PA_ERROR_INVALID_ARGUMENT, fn + ": int8 cache needs scales and absmax");
+        if (cfg->num_kv_heads > 65535) return set_error(PA_ERROR_INVALID_CONFIG, fn + ": too many KV heads");
+        dim3 grid(n_tok, cfg->num_kv_heads, 2);
+        auto* kc = static_cast<int8_t*>(k_cache);
+        auto* vc = static_cast<int8_t*>(v_cache);
+        switch (cfg->head_dim) {
+            case 64:
+                append_int8_kernel<64><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc, k_scale,
+                                                           v_scale, k_absmax, v_absmax, cfg->num_kv_heads, capacity,
+                                                           tok_stride);
+                break;
+            case 128:
+                append_int8_kernel<128><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                            k_scale, v_scale, k_absmax, v_absmax, cfg->num_kv_heads,
+                                                            capacity, tok_stride);
+                break;
+            default:
+                append_int8_kernel<256><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                            k_scale, v_scale, k_absmax, v_absmax, cfg->num_kv_heads,
+                                                            capacity, tok_stride);
+                break;
+        }
+    }
+    PA_HIP_CHECK(hipGetLastError());
+    return clear_error();
+}
+
+}  // namespace pa
+
+extern "C" {
 
 pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg, const void* k_new, const void* v_new,
                        const int64_t* slot_mapping, int32_t n_tok, void* k_cache, void* v_cache,
                        float* k_scale, float* v_scale, float* k_absmax, float* v_absmax) {
     pa_status st = pa::check_config(cfg, "pa_kv_append");
     if (st != PA_SUCCESS) return st;
-    if (n_tok < 0) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: n_tok < 0");
-    if (n_tok == 0) return pa::clear_error();
-    if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache)
-        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: null pointer");
-    const int64_t capacity = static_cast<int64_t>(cfg->num_blocks) * pa::kBlockSize;
-    const bool in_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
-    hipStream_t s = pa::native(stream);
-    if (cfg->kv_dtype != PA_DTYPE_INT8) {
-        dim3 grid(n_tok, 2);
-        append_plain_kernel<<<grid, 256, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, k_cache, v_cache,
-                                                  cfg->kv_dtype == PA_DTYPE_BF16, cfg->num_kv_heads,
-                                                  cfg->head_dim, capacity);
-    } else {
-        if (!k_scale || !v_scale || !k_absmax || !v_absmax)
-            return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_kv_append: int8 cache needs scales and absmax");
-        if (cfg->num_kv_heads > 65535)
-            return pa::set_error(PA_ERROR_INVALID_CONFIG, "pa_kv_append: too many KV heads");
-        dim3 grid(n_tok, cfg->num_kv_heads, 2);
-        auto* kc = static_cast<int8_t*>(k_cache);
-        auto* vc = static_cast<int8_t*>(v_cache);
-        switch (cfg->head_dim) {
-            case 64:
-                append_int8_kernel<64><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
-                                                           k_scale, v_scale, k_absmax, v_absmax,
-                                                           cfg->num_kv_heads, capacity);
-                break;
-            case 128:
-                append_int8_kernel<128><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
-                                                            k_scale, v_scale, k_absmax, v_absmax,
-                                                            cfg->num_kv_heads, capacity);
-                break;
-            default:
-                append_int8_kernel<256><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
-                                                            k_scale, v_scale, k_absmax, v_absmax,
-                                                            cfg->num_kv_heads, capacity);
-                break;
-        }
-    }
-    PA_HIP_CHECK(hipGetLastError());
-    return pa::clear_error();
+    return pa::launch_kv_append("pa_kv_append", pa::native(stream), cfg, k_new, v_new, cfg->q_dtype == PA_DTYPE_BF16,
+                                static_cast<int64_t>(cfg->num_kv_heads) * cfg->head_dim, slot_mapping, n_tok,
+                                k_cache, v_cache, k_scale, v_scale, k_absmax, v_absmax);
 }
 
 }  // extern "C"

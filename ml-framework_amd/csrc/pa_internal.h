@@ -47,6 +47,12 @@ constexpr int kBlockSize = 16;
 
 // Validates the fields every operator needs; on failure sets the last error.
 pa_status check_config(const pa_config* cfg, const char* fn);
+// The append of pa_kv_append on stream s, for new K/V whose token t starts at t * tok_stride
+// elements (pa_kv_append: num_kv_heads * head_dim); in_bf16 selects the activation dtype.
+pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, const void* k_new, const void* v_new,
+                           bool in_bf16, int64_t tok_stride, const int64_t* slot_mapping, int32_t n_tok,
+                           void* k_cache, void* v_cache, float* k_scale, float* v_scale, float* k_absmax,
+                           float* v_absmax);
 
 inline float resolve_scale(const pa_config* cfg) {
     // StandardPagedAttentionKernel.cs:18,28 -- scale > 0 overrides 1/sqrt(headDim).

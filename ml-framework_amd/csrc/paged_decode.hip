@@ -146,7 +146,8 @@ __global__ __launch_bounds__(64) void append_last_token_int8_kernel(const Decode
         const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), k);
         return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
     };
-    pa::append_int8_segment<D>(is_v ? a.v_new : a.k_new, a.q_bf16 != 0, slot_at, i,
+    pa::append_int8_segment<D>(is_v ? a.v_new : a.k_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D,
+                               slot_at, i,
                                num_seqs, static_cast<int8_t*>(const_cast<void*>(is_v ? a.v_cache : a.k_cache)),
                                const_cast<float*>(is_v ? a.v_scale : a.k_scale), is_v ? a.v_absmax : a.k_absmax,
                                static_cast<int>(blockIdx.y), a.num_kv_heads, capacity, is_v);

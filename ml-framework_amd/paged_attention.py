@@ -55,6 +55,7 @@ EXPORTS = (
     "pa_paged_decode_append", "pa_chunked_prefill",
     "pa_block_bytes", "pa_copy_blocks", "pa_gather_blocks", "pa_scatter_blocks", "pa_read_block_f32",
     "pa_write_block_f32",
+    "pa_qkv_workspace_size", "pa_qkv_project_append", "pa_o_workspace_size", "pa_o_project",
 )
 
 
@@ -146,6 +147,10 @@ _SIGNATURES = {
     "pa_scatter_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32, _P],
     "pa_read_block_f32": [_P, _CFG, _P, _P, _P, _P, _I32, _I32, _P, _P],
     "pa_write_block_f32": [_P, _CFG, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P],
+    "pa_qkv_workspace_size": [_CFG, _I32, ctypes.POINTER(_SZ)],
+    "pa_qkv_project_append": [_P, _CFG, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ],
+    "pa_o_workspace_size": [_CFG, _I32, ctypes.POINTER(_SZ)],
+    "pa_o_project": [_P, _CFG, _P, _P, _I32, _I32, _P, _P, _SZ],
 }
 
 _lib = None
@@ -376,6 +381,31 @@ def write_block_f32(stream, cfg: PaConfig, k_cache, v_cache, k_scale, v_scale, k
                     k_in, v_in):
     call("pa_write_block_f32", stream.handle if stream else None, ctypes.byref(cfg), _ptr(k_cache), _ptr(v_cache),
          _ptr(k_scale), _ptr(v_scale), _ptr(k_absmax), _ptr(v_absmax), block, tokens, _ptr(k_in), _ptr(v_in))
+
+
+# ---- projections either side of attention ----------------------------------------------------
+def qkv_workspace_size(cfg: PaConfig, n_tok: int) -> int:
+    n = ctypes.c_size_t()
+    call("pa_qkv_workspace_size", ctypes.byref(cfg), n_tok, ctypes.byref(n))
+    return n.value
+
+
+def qkv_project_append(stream, cfg: PaConfig, x, w_qkv, hidden, n_tok, slot_mapping, q_out, k_cache, v_cache,
+                       k_scale, v_scale, k_absmax, v_absmax, workspace, workspace_bytes):
+    call("pa_qkv_project_append", stream.handle if stream else None, ctypes.byref(cfg), _ptr(x), _ptr(w_qkv), hidden,
+         n_tok, _ptr(slot_mapping), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+         _ptr(k_absmax), _ptr(v_absmax), _ptr(workspace), workspace_bytes)
+
+
+def o_workspace_size(cfg: PaConfig, n_tok: int) -> int:
+    n = ctypes.c_size_t()
+    call("pa_o_workspace_size", ctypes.byref(cfg), n_tok, ctypes.byref(n))
+    return n.value
+
+
+def o_project(stream, cfg: PaConfig, attn, w_o, hidden, n_tok, y, workspace, workspace_bytes):
+    call("pa_o_project", stream.handle if stream else None, ctypes.byref(cfg), _ptr(attn), _ptr(w_o), hidden, n_tok,
+         _ptr(y), _ptr(workspace), workspace_bytes)
 
 
 @dataclass

@@ -237,3 +237,10 @@ def read_block_f32(cfg, k_cache, v_cache, k_scale, v_scale, block, tokens):
         vt = vt.astype(np.float32) * v_scale[block][:, None, None]
     return (np.ascontiguousarray(np.transpose(kt, (1, 0, 2)).astype(np.float32)),
             np.ascontiguousarray(np.transpose(vt, (2, 0, 1)).astype(np.float32)))
+
+
+# ---- projections either side of attention (numpy) ----------------------------------------------
+def linear(x, w):
+    """Linear.Forward without bias (src/MLFramework/Modules/Linear.cs:81-110): y = x W^T, here in
+    float64 from the given (bf16-valued) operands; x [n][in], w [out][in]."""
+    return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
