@@ -124,9 +124,67 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     };
     // Q^T operand: lane (q4, n) holds head n, dims k_dim0(s, q4) .. +8 of slab s (zero rows for n >= G).
     bf16x8_t qhi[NSLAB], qlo[QF32 ? NSLAB : 1];
+    // int8 caches: the K codes go to v_mfma_i32_16x16x64_i8 as they are, against Q as a 16-bit fixed
+    // point number in two int8 digits: q ~ q_sq * (256 hi + lo), q_sq = max|q| of the head / 32639,
+    // so S = q_sq (256 K.hi + K.lo) exactly in int32 (per score an error of at most q_sq / 2 per
+    // dim times |code|, about 2e-5 of max|q| 127 sqrt(D)). Slab t covers the lane's dims
+    // k_dim0(2t, q4) .. +16, i.e. K registers 2t and 2t + 1.
+    constexpr int NI8 = NSLAB / 2;
+    i32x4_t qdh[KV == PA_DTYPE_INT8 ? NI8 : 1], qdl[KV == PA_DTYPE_INT8 ? NI8 : 1];
+    float q_sq = 0.0f;
+    auto int8_q_digits = [&](const float (&x)[NSLAB][8]) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < NSLAB; sl++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(x[sl][e]));
+        mx = rows_max(mx);  // max |q| of head n
+        q_sq = mx * (1.0f / 32639.0f);
+        const float inv = mx > 0.0f ? 32639.0f / mx : 0.0f;
+#pragma unroll
+        for (int t = 0; t < NI8; t++) {
+            uint32_t wh[4], wl[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                wh[w] = 0;
+                wl[w] = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int e = 4 * w + b;  // dim e of the slab's 16
+                    const int q16 = static_cast<int>(__builtin_rintf(x[2 * t + (e >> 3)][e & 7] * inv));
+                    const int lo = ((q16 + 128) & 255) - 128;
+                    const int hi = (q16 - lo) >> 8;
+                    wh[w] |= (static_cast<uint32_t>(hi) & 255u) << (8 * b);
+                    wl[w] |= (static_cast<uint32_t>(lo) & 255u) << (8 * b);
+                }
+            }
+            qdh[t] = __builtin_bit_cast(i32x4_t, make_uint4(wh[0], wh[1], wh[2], wh[3]));
+            qdl[t] = __builtin_bit_cast(i32x4_t, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+        }
+    };
     auto side_loads = [&]() {
         const bool hv = n < G;
         const int64_t qrow = (static_cast<int64_t>(seq) * Hkv * G + kvh * G + (hv ? n : 0)) * D;
+        if constexpr (KV == PA_DTYPE_INT8) {
+            float x[NSLAB][8];
+#pragma unroll
+            for (int s = 0; s < NSLAB; s++) {
+                const int d0 = k_dim0<D>(s, q4);
+                if constexpr (QF32) {
+                    const float* qp = static_cast<const float*>(a.q) + qrow + d0;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[s][e] = hv ? qp[e] : 0.0f;
+                } else {
+                    const uint4 raw = hv ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
+                                         : make_uint4(0, 0, 0, 0);
+                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        x[s][e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+                }
+            }
+            int8_q_digits(x);
+        } else {
 #pragma unroll
         for (int s = 0; s < NSLAB; s++) {
             const int d0 = k_dim0<D>(s, q4);
@@ -150,6 +208,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                                      : make_uint4(0, 0, 0, 0);
                 qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
             }
+        }
         }
         if constexpr (KV == PA_DTYPE_INT8) {  // unconditional: an invalid block's scales are never used
             const int sb = my_bid >= 0 && my_bid < a.num_blocks ? my_bid : 0;
@@ -249,18 +308,32 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         }
         // S^T[token 4q4+i][head n]
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (KV == PA_DTYPE_INT8) {
+            i32x4_t ch = {0, 0, 0, 0}, cl = {0, 0, 0, 0};
 #pragma unroll
-        for (int sl = 0; sl < NSLAB; sl++) {
-            const bf16x8_t kop = k_operand(kr[sl]);
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
-            if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+            for (int t = 0; t < NI8; t++) {
+                const i32x4_t kop = __builtin_bit_cast(i32x4_t, make_uint4(kr[2 * t].x, kr[2 * t].y, kr[2 * t + 1].x,
+                                                                            kr[2 * t + 1].y));
+                ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qdh[t], ch, 0, 0, 0);
+                cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qdl[t], cl, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                s[i] = static_cast<float>(ch[i] * 256 + cl[i]);  // |.| < 127 * 32639 * D < 2^31
+        } else {
+#pragma unroll
+            for (int sl = 0; sl < NSLAB; sl++) {
+                const bf16x8_t kop = k_operand(kr[sl]);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[sl], s, 0, 0, 0);
+                if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
+            }
         }
         const int tbase = (g.b0 + e) * 16 + 4 * q4;
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float v = s[i];
-            if constexpr (KV == PA_DTYPE_INT8) v = v * ks;  // (q . code) * k_scale, then * scale
+            if constexpr (KV == PA_DTYPE_INT8) v = v * (ks * q_sq);  // (Q16 . code) q_sq k_scale, then * scale
             v = v * a.scale;
             sc[i] = tbase + i < T ? v : -INFINITY;
         }
