@@ -97,6 +97,9 @@ def make_inputs(w: wl.Workload, seed: int):
     else:
         out["k_cache"] = randn(nb, Hkv, 16, D)
         out["v_cache"] = randn(nb, Hkv, 16, D)
+    # The library runs on its own stream: torch's kernels (and the temporaries they free on enqueue,
+    # whose memory torch hands out again at once) must be done before any of it is used there.
+    torch.cuda.synchronize()
     return out
 
 
@@ -115,6 +118,7 @@ class Timer:
     def __call__(self, fn, steps, warmup):
         import torch
 
+        torch.cuda.synchronize()  # buffers allocated through torch are settled before the library's stream runs
         for _ in range(warmup):
             fn()
         self.stream.synchronize()
@@ -170,6 +174,38 @@ def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
            "context_tokens": int(w.context_lens.sum()), "num_seqs": w.num_seqs,
            "step": "pa_paged_decode_append" if fused else "pa_paged_decode"}
     del inp, out, ws
+    return res
+
+
+def run_prefix_decode(w, timer, stream, steps, warmup, seed):
+    """C5 through pa_paged_decode_prefix: the sequences' shared blocks are read once per group of
+    16 / G sequences; same inputs, output and algorithmic (distinct) bytes as the plain decode."""
+    import torch
+
+    inp = make_inputs(w, seed)
+    cfg = config_of(w)
+    S = w.num_seqs
+    links = np.zeros(S, np.int32)
+    links[1:] = w.shared_prefix_blocks
+    pb = pa.prefix_plan_bytes(S)
+    plan = torch.empty((max(pb, 4),), dtype=torch.uint8, device="cuda:0")
+    out = torch.empty((S, w.num_q_heads, w.head_dim), dtype=torch.float32, device="cuda:0")
+    wsb = pa.prefix_workspace_size(cfg, S, w.max_context_len)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device="cuda:0")
+    torch.cuda.synchronize()
+    ng = pa.prefix_plan_build(stream, cfg, links, plan, pb)
+
+    def step():
+        pa.paged_decode_prefix(stream, cfg, out, inp["q"], inp["k_cache"], inp["v_cache"], inp["k_scale"],
+                               inp["v_scale"], inp["tables"], inp["lens"], S, w.max_blocks, w.max_context_len,
+                               plan, ng, ws, wsb)
+
+    ms = timer(step, steps, warmup)
+    nbytes = w.decode_algorithmic_bytes()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    res = {"us_per_layer_step": round(ms * 1e3, 3), "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1),
+           "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "groups": ng, "step": "pa_paged_decode_prefix"}
+    del inp, out, ws, plan
     return res
 
 
@@ -500,6 +536,8 @@ def main():
             c5["logical_gbps"] = round(logical / (c5["us_per_layer_step"] * 1e-6) / 1e9, 1)
             extra["C5"] = c5
             log(f"[bench] C5 {c5['us_per_layer_step']} us")
+            extra["C5_prefix"] = run_prefix_decode(w5, timer, stream, n, args.warmup, 5)
+            log(f"[bench] C5 shared-prefix decode {extra['C5_prefix']['us_per_layer_step']} us")
             extra["C3"] = run_c3(timer, stream, n, args.warmup, 3)
             log(f"[bench] C3 {extra['C3']['us_per_layer_step']} us")
             extra["block_moves"] = run_block_moves(timer, stream, n, args.warmup, 4)

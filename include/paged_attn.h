@@ -251,6 +251,45 @@ pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float*
                                  int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
                                  void* workspace, size_t workspace_bytes);
 
+/* ---- Shared-prefix decode ----
+ * Sequences forked from one parent share the parent's first physical blocks (copy-on-write:
+ * the same block ids lead their tables; BlockShareManager.ShareBlock,
+ * Inference/PagedAttention/Sharing/BlockShareManager.cs:34-54, keeps the refcounts). The result
+ * is that of pa_paged_decode; the shared blocks are read once per group of up to 16 / G
+ * sequences (G = num_q_heads / num_kv_heads) instead of once per sequence. No reference
+ * counterpart: the reference decodes every sequence over its whole table. */
+
+/* Bytes of the device plan for num_seqs sequences. */
+pa_status pa_prefix_plan_bytes(int32_t num_seqs, size_t* bytes);
+
+/* Builds the plan into `plan` (device memory, plan_bytes >= pa_prefix_plan_bytes) from the host
+ * array shared_with_prev[num_seqs]: shared_with_prev[s] = number of leading block-table entries
+ * sequence s has in common with sequence s - 1 (entry 0 is ignored; 0 = no link). Linked runs
+ * are cut into groups of at most 16 / G sequences sharing the run's minimum link; *num_groups
+ * receives the group count to pass to pa_paged_decode_prefix. The plan depends only on the
+ * grouping, not on the context lengths, so it is rebuilt only when sequences fork or leave.
+ * Synchronises `stream` (host-to-device copy); refused while the stream captures a graph. */
+pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t num_seqs,
+                               const int32_t* shared_with_prev, void* plan, size_t plan_bytes,
+                               int32_t* num_groups);
+
+/* Workspace of pa_paged_decode_prefix for up to num_seqs sequences of up to max_context_len. */
+pa_status pa_prefix_workspace_size(const pa_config* cfg, int32_t num_seqs, int32_t max_context_len,
+                                   size_t* bytes);
+
+/* pa_paged_decode over the same arguments plus a plan from pa_prefix_plan_build (same num_seqs
+ * and head ratio). Contract: within a group the shared block ids are identical in every table
+ * and every member's context_len covers the shared blocks (>= 16 * shared); a plan that breaks
+ * it gives wrong attention but never reads outside the arguments. BF16 or INT8 caches;
+ * num_seqs + num_groups <= 2047; cfg->partition_size is not used (equal ranges per worker). */
+pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                 const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
+                                 const void* plan, int32_t num_groups,
+                                 void* workspace, size_t workspace_bytes);
+
 /* Chunked prefill: prefill sequence s has chunk_len[s] = q_start_loc[s+1] - q_start_loc[s] new
  * query tokens at absolute positions prefix_lens[s] + i; the chunk's K/V must already be appended,
  * so keys are positions [0, prefix_lens[s] + chunk_len[s]) read through block_tables[s].

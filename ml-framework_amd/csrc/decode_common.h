@@ -46,7 +46,25 @@ struct DecodeArgs {
     int32_t split_grid;  // workers (waves) of the launch
     int32_t q_bf16;
     float scale;
+    // shared-prefix decode (pa_paged_decode_prefix): the plan (prefix groups, then per sequence
+    // its group and shared block count) and its group count; unused by the other entry points.
+    const int32_t* plan;
+    int32_t num_groups;
+    // Slot of row r, KV head h when the row lies whole inside one range: row_slot_base + r * Hkv +
+    // h (a range has slots for its first and last row portions only, and grouped rows never write
+    // the output directly).
+    int32_t row_slot_base;
 };
+
+// Shared-prefix plan, in device memory: num_groups records {first sequence, members, shared
+// blocks}, then per sequence {group or -1, shared blocks or 0}. The members of a group are
+// consecutive sequences whose block tables agree on the shared blocks; with G query heads per KV
+// head a group has at most 16 / G members (one MFMA column tile of query heads).
+constexpr int kPlanGroupInts = 3;
+constexpr int kPlanSeqInts = 2;
+// Workspace slot width of the shared-prefix decode: a slot holds the 16 MFMA columns (the query
+// heads of up to 16 / G sequences) of one KV head.
+constexpr int kPrefixSlotRows = 16;
 
 // Context length clamped to what the table holds and to max_context_len (raw: context_lens[seq]).
 __device__ __forceinline__ int clamp_len(const DecodeArgs& a, int raw) {
@@ -208,9 +226,13 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
     const int kvh = blockIdx.x, seq = blockIdx.y;
     const int64_t R0 = a.ws_pref[seq];
     const int nbr = a.ws_pref[seq + 1] - a.ws_pref[seq];
+    const int64_t total = a.ws_pref[num_seqs];
     if (nbr <= 0) return;
+    // The prefix table comes from the decode launch through the workspace: one that does not fit
+    // (the workspace overwritten in between) is not followed outside the slots.
+    if (R0 < 0 || R0 + nbr > total) return;
     const int Hkv = a.num_kv_heads;
-    const int64_t C = split_range_blocks(a, a.ws_pref[num_seqs]);
+    const int64_t C = split_range_blocks(a, total);
     const int64_t w1 = R0 / C, w2 = (R0 + nbr - 1) / C;
     if (w1 == w2) return;  // written whole by the decode kernel
     const bool starts_inside = R0 != w1 * C;
@@ -218,6 +240,69 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
     merge_partitions<D>(a, seq, kvh, static_cast<int>(w2 - w1 + 1), [&](int u, int g) {
         const int64_t unit = (w1 + u) * Hkv + kvh;
         return (2 * unit + (u == 0 && starts_inside ? 1 : 0)) * G + g;
+    });
+}
+
+// Shared-prefix decode merge: one workgroup per (KV head, sequence). Rows of the decode's list
+// are the num_groups prefix rows, then one suffix row per sequence (its blocks after the shared
+// ones); every row's partials sit in 16-wide slots (slot 2u + {0, 1} of unit u, as above, or the
+// row's own slot row_slot_base + r * Hkv + kvh when the row lies inside one range). A
+// sequence in a group combines its suffix row's partials with those of its group's prefix row
+// (columns mi * G .. mi * G + G - 1, mi its place in the group); an ungrouped sequence whose row
+// was written whole by the decode is skipped.
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_prefix_kernel(const DecodeArgs a, int32_t num_seqs) {
+    const int kvh = blockIdx.x, seq = blockIdx.y;
+    if (clamp_len(a, a.context_lens[seq]) <= 0) return;  // zero output, written by the decode
+    const int NG = a.num_groups;
+    const int Hkv = a.num_kv_heads, G = a.group;
+    const int32_t* groups = a.plan;
+    const int32_t* seqinfo = a.plan + static_cast<int64_t>(NG) * kPlanGroupInts;
+    int grp = seqinfo[static_cast<int64_t>(seq) * kPlanSeqInts];
+    if (grp >= NG) grp = -1;
+    const int row = NG + seq;
+    const int64_t total = a.ws_pref[NG + num_seqs];
+    const int64_t C = split_range_blocks(a, total);
+    const int64_t R0 = a.ws_pref[row];
+    const int nbr = a.ws_pref[row + 1] - a.ws_pref[row];
+    if (R0 < 0 || nbr < 0 || R0 + nbr > total) return;  // a prefix table that does not fit the slots
+    int ns = 0;
+    int64_t w1 = 0;
+    bool s_inside = false;
+    if (nbr > 0) {
+        w1 = R0 / C;
+        ns = static_cast<int>((R0 + nbr - 1) / C - w1 + 1);
+        s_inside = R0 != w1 * C;
+    }
+    int np = 0, mi = 0;
+    int64_t pw1 = 0;
+    bool p_inside = false;
+    if (grp >= 0) {
+        const int64_t P0 = a.ws_pref[grp];
+        const int pn = a.ws_pref[grp + 1] - a.ws_pref[grp];
+        if (P0 < 0 || pn < 0 || P0 + pn > total) return;
+        mi = seq - groups[static_cast<int64_t>(grp) * kPlanGroupInts];
+        if (mi < 0 || (mi + 1) * G > kPrefixSlotRows) return;  // not a member: a plan that does not fit
+        if (pn > 0) {
+            pw1 = P0 / C;
+            np = static_cast<int>((P0 + pn - 1) / C - pw1 + 1);
+            p_inside = P0 != pw1 * C;
+        }
+    }
+    if (grp < 0 && ns <= 1) return;  // written whole by the decode kernel
+    if (ns + np == 0) return;
+    // A row inside one range left its partial in its row slot, a split row one per range.
+    merge_partitions<D>(a, seq, kvh, ns + np, [&](int u, int g) -> int64_t {
+        if (u < ns) {
+            if (ns == 1) return (a.row_slot_base + static_cast<int64_t>(row) * Hkv + kvh) * kPrefixSlotRows + g;
+            const int64_t unit = (w1 + u) * Hkv + kvh;
+            return (2 * unit + (u == 0 && s_inside ? 1 : 0)) * kPrefixSlotRows + g;
+        }
+        u -= ns;
+        if (np == 1)
+            return (a.row_slot_base + static_cast<int64_t>(grp) * Hkv + kvh) * kPrefixSlotRows + mi * G + g;
+        const int64_t unit = (pw1 + u) * Hkv + kvh;
+        return (2 * unit + (u == 0 && p_inside ? 1 : 0)) * kPrefixSlotRows + mi * G + g;
     });
 }
 
@@ -311,12 +396,14 @@ int device_cus();
 // bf16 / int8 caches; num_seqs < kMaxPersistentSeqs. Launches the resident workgroups, each of
 // decode_waves(D) independent workers, with no more than kMaxDecodeWorkers and max_units workers
 // in all; records the worker count in a.split_grid (the merge kernel needs it).
-void launch_decode_mfma_d64(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
-                            hipStream_t s);
-void launch_decode_mfma_d128(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
-                             hipStream_t s);
-void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs, int64_t max_grid,
-                             hipStream_t s);
+// shared: the shared-prefix decode (a.plan, a.num_groups; no append), whose row list is the
+// num_groups prefix rows and then one suffix row per sequence.
+void launch_decode_mfma_d64(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
+                            int64_t max_grid, hipStream_t s);
+void launch_decode_mfma_d128(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
+                             int64_t max_grid, hipStream_t s);
+void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
+                             int64_t max_grid, hipStream_t s);
 // fp32 caches: grid (max_parts, Hkv, num_seqs); returns false for an uncompiled shape.
 bool launch_decode_fp32(const DecodeArgs& a, int head_dim, dim3 grid, hipStream_t s);
 

@@ -35,9 +35,20 @@ namespace pa {
 // while the O accumulators are rescaled on few blocks instead of on most of them.
 constexpr float kRescaleThreshold = 8.0f;
 
+template <bool SHARED>
 struct MfmaShared {
-    int pref[kMaxPersistentSeqs + 1];  // blocks (per KV head row) before sequence s
-    int lens[kMaxPersistentSeqs];      // clamped context length of sequence s
+    int pref[kMaxPersistentSeqs + 1];  // blocks (per KV head row) before row r
+    int lens[kMaxPersistentSeqs];      // token bound of row r's blocks (clamped context length)
+};
+// Shared-prefix decode rows: row r starts at block boff[r] of sequence seq0[r]'s table and its
+// query columns are the heads of sequences seq0[r] .. seq0[r] + nmem - 1 (qinfo = seq0 | nmem << 16
+// | grouped << 24; grouped rows always leave partials).
+template <>
+struct MfmaShared<true> {
+    int pref[kMaxPersistentSeqs + 1];
+    int lens[kMaxPersistentSeqs];
+    int boff[kMaxPersistentSeqs];
+    int qinfo[kMaxPersistentSeqs];
 };
 
 // Blocks [b0, b1) of row (seq, kvh), at most kPieceBlocks of them. slot < 0: the portion the
@@ -46,6 +57,7 @@ struct MfmaShared {
 struct Piece {
     int seq, kvh, b0, b1, T, slot;
     bool last;
+    int nmem;  // shared-prefix decode: query columns are the heads of sequences seq .. seq + nmem - 1
 };
 
 constexpr int kPieceBlocks = 64;  // one block id per lane
@@ -79,7 +91,7 @@ struct RowState {
 // One piece, streamed by one wave; my_bid = piece_ids(..). prefetch_next() is called once, after
 // the piece's first loads, to start the next piece's id loads. s_new: this wave's LDS staging of
 // the appended token (2 * D floats).
-template <int D, int KV, bool QF32, bool APPEND, typename Prefetch>
+template <int D, int KV, bool QF32, bool APPEND, bool SHARED, typename Prefetch>
 __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, int my_bid, RowState<D / 16>& st,
                                            float* s_new, Prefetch&& prefetch_next) {
     using Raw = MfmaRaw<KV>;
@@ -162,9 +174,14 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             qdl[t] = __builtin_bit_cast(i32x4_t, make_uint4(wl[0], wl[1], wl[2], wl[3]));
         }
     };
+    // Column n's query head: head n of the sequence, or (shared-prefix rows) head n % G of member
+    // n / G.
+    const int ncol = SHARED ? g.nmem * G : G;
     auto side_loads = [&]() {
-        const bool hv = n < G;
-        const int64_t qrow = (static_cast<int64_t>(seq) * Hkv * G + kvh * G + (hv ? n : 0)) * D;
+        const bool hv = n < ncol;
+        const int mi = SHARED && hv ? n / G : 0;
+        const int64_t qrow =
+            (static_cast<int64_t>(seq + mi) * Hkv * G + kvh * G + (hv ? n - mi * G : 0)) * D;
         if constexpr (KV == PA_DTYPE_INT8) {
             float x[NSLAB][8];
 #pragma unroll
@@ -429,18 +446,18 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         M[i] = __shfl(m_run, 4 * q4 + i, 64);
         L[i] = __shfl(l_tot, 4 * q4 + i, 64);
     }
-    if (4 * q4 < G) {
+    if (4 * q4 < ncol) {
         const int64_t row0 = static_cast<int64_t>(seq) * Hkv * G + kvh * G;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int h = 4 * q4 + i;
-            if (h >= G) break;
+            if (h >= ncol) break;
             if (g.slot < 0) {
                 const float inv = 1.0f / L[i];
 #pragma unroll
                 for (int t = 0; t < NT; t++) a.out[(row0 + h) * D + 16 * t + n] = acc[t][i] * inv;
             } else {
-                const int64_t pidx = static_cast<int64_t>(g.slot) * G + h;
+                const int64_t pidx = static_cast<int64_t>(g.slot) * (SHARED ? kPrefixSlotRows : G) + h;
 #pragma unroll
                 for (int t = 0; t < NT; t++) a.ws_o[pidx * D + 16 * t + n] = acc[t][i];
                 if (n == 0) {
@@ -453,13 +470,15 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     st.reset();
 }
 
-// Persistent decode kernel over at most kMaxPersistentSeqs - 1 sequences.
-template <int D, int KV, bool QF32, bool APPEND>
+// Persistent decode kernel over at most kMaxPersistentSeqs - 1 rows: the sequences, or (SHARED)
+// the plan's prefix rows followed by one suffix row per sequence.
+template <int D, int KV, bool QF32, bool APPEND, bool SHARED>
 __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_decode_mfma_persistent_kernel(const DecodeArgs a,
                                                                                              int32_t num_seqs) {
+    static_assert(!(APPEND && SHARED), "the shared-prefix decode does not append");
     constexpr int WAVES = decode_waves(D);
     constexpr int THREADS = 64 * WAVES;
-    __shared__ MfmaShared sh;
+    __shared__ MfmaShared<SHARED> sh;
     __shared__ float s_app[WAVES][2 * D];  // per wave: the appended token's K and V values
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -468,19 +487,63 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     // All PER lengths are loaded before any is used, so the loads overlap (a use between them would
     // serialise PER memory round trips).
     constexpr int PER = (kMaxPersistentSeqs + THREADS - 1) / THREADS;
-    int raw[PER];
+    const int NG = SHARED ? a.num_groups : 0;
+    const int R = NG + num_seqs;  // rows
+    const int G = a.group;
+    // Row r's record: the context length (and, SHARED, the sequence's {group, shared blocks}), or
+    // a prefix row's group {first sequence, members, shared blocks}.
+    int raw[PER], x1[PER], x2[PER];
 #pragma unroll
-    for (int k = 0; k < PER; k++) raw[k] = a.context_lens[min(tid * PER + k, num_seqs - 1)];
+    for (int k = 0; k < PER; k++) {
+        const int r = min(tid * PER + k, R - 1);
+        x1[k] = 0;
+        x2[k] = 0;
+        if (SHARED && r < NG) {
+            const int32_t* gr = a.plan + static_cast<int64_t>(r) * kPlanGroupInts;
+            raw[k] = gr[0];
+            x1[k] = gr[1];
+            x2[k] = gr[2];
+        } else {
+            raw[k] = a.context_lens[r - NG];
+            if constexpr (SHARED) {
+                const int32_t* si = a.plan + static_cast<int64_t>(NG) * kPlanGroupInts +
+                                    static_cast<int64_t>(r - NG) * kPlanSeqInts;
+                x1[k] = si[0];
+                x2[k] = si[1];
+            }
+        }
+    }
     int cnt[PER];
     int local = 0;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        const int s = tid * PER + k;
+        const int r = tid * PER + k;
         int c = 0;
-        if (s < num_seqs) {
-            const int T = clamp_len(a, raw[k]);
-            sh.lens[s] = T;
-            c = T <= 0 ? 0 : (T + 15) / 16;
+        if (r < R) {
+            if (SHARED && r < NG) {
+                // A record that does not fit the call (members beyond num_seqs, more columns than
+                // one MFMA tile, no shared block) gives an empty row.
+                const int first = raw[k], nm = x1[k];
+                const bool ok = first >= 0 && nm >= 2 && nm * G <= 16 && first <= num_seqs - nm && x2[k] > 0;
+                const int T = ok ? clamp_len(a, min(x2[k], a.max_blocks_per_seq) * 16) : 0;
+                sh.lens[r] = T;
+                c = T <= 0 ? 0 : (T + 15) / 16;
+                if constexpr (SHARED) {
+                    sh.boff[r] = 0;
+                    sh.qinfo[r] = (ok ? first : 0) | (ok ? nm : 1) << 16 | 1 << 24;
+                }
+            } else {
+                const int T = clamp_len(a, raw[k]);
+                sh.lens[r] = T;
+                c = T <= 0 ? 0 : (T + 15) / 16;
+                if constexpr (SHARED) {
+                    const bool grouped = x1[k] >= 0 && x1[k] < NG;
+                    const int skip = grouped ? min(max(x2[k], 0), c) : 0;
+                    c -= skip;
+                    sh.boff[r] = skip;
+                    sh.qinfo[r] = (r - NG) | 1 << 16 | (grouped ? 1 : 0) << 24;
+                }
+            }
         }
         cnt[k] = c;
         local += c;
@@ -499,10 +562,10 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     int run = wave_off + incl - local;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        const int s = tid * PER + k;
-        if (s <= num_seqs) {
-            sh.pref[s] = run;
-            if (blockIdx.x == 0) a.ws_pref[s] = run;  // read by the merge kernel
+        const int r = tid * PER + k;
+        if (r <= R) {
+            sh.pref[r] = run;
+            if (blockIdx.x == 0) a.ws_pref[r] = run;  // read by the merge kernel
         }
         run += cnt[k];
     }
@@ -511,7 +574,7 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     const int Hkv = a.num_kv_heads;
     // Sequences with no context produce zeros.
     for (int s = blockIdx.x; s < num_seqs; s += gridDim.x) {
-        if (sh.lens[s] > 0) continue;
+        if (sh.lens[NG + s] > 0) continue;
         const int n = Hkv * a.group * D;
         for (int idx = tid; idx < n; idx += THREADS) a.out[static_cast<int64_t>(s) * n + idx] = 0.0f;
     }
@@ -520,7 +583,7 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     // sequence-major block list for KV head kvh, on worker u (mod the worker count W). Workers
     // u .. u + Hkv - 1 run together and read the same physical blocks (all KV heads of a block are
     // one contiguous Hkv * 16 * D run). From here on every wave works alone.
-    const int64_t total = sh.pref[num_seqs];
+    const int64_t total = sh.pref[R];
     if (total == 0) return;
     const int64_t W = a.split_grid;
     const int64_t C = split_range_blocks(a, total);
@@ -534,7 +597,7 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     // search, so a worker whose range lies far into the batch does not start late behind a chain of
     // dependent LDS reads.
     auto locate = [&](int64_t pos) {
-        int lo = 0, hi = num_seqs;  // pref[lo] <= pos < pref[hi]
+        int lo = 0, hi = R;  // pref[lo] <= pos < pref[hi]
         while (hi - lo > 1) {
             const int h = (lo + hi) >> 1;
             if (sh.pref[h] <= pos) lo = h;
@@ -561,12 +624,20 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
             const int nbr = sh.pref[seq + 1] - sh.pref[seq];
             const int pb0 = static_cast<int>(p - sh.pref[seq]);
             prow_end = static_cast<int>(min(static_cast<int64_t>(nbr), pb0 + (end - p)));
-            pslot = (pb0 == 0 && prow_end == nbr) ? -1 : static_cast<int>(2 * u + (p == r * C ? 0 : 1));
+            bool grouped = false;
+            if constexpr (SHARED) grouped = (sh.qinfo[seq] >> 24) != 0;
+            if (pb0 == 0 && prow_end == nbr) pslot = grouped ? a.row_slot_base + seq * Hkv + kvh : -1;  // whole row
+            else pslot = static_cast<int>(2 * u + (p == r * C ? 0 : 1));
         }
         const int b0 = static_cast<int>(p - sh.pref[seq]);
         const int b1 = min(prow_end, b0 + kPieceBlocks);
         mid = b1 < prow_end;
-        g = Piece{seq, kvh, b0, b1, sh.lens[seq], pslot, !mid};
+        if constexpr (SHARED) {
+            const int qi = sh.qinfo[seq], bo = sh.boff[seq];
+            g = Piece{qi & 0xffff, kvh, bo + b0, bo + b1, sh.lens[seq], pslot, !mid, (qi >> 16) & 0xff};
+        } else {
+            g = Piece{seq, kvh, b0, b1, sh.lens[seq], pslot, !mid, 1};
+        }
         p += b1 - b0;
         return true;
     };
@@ -580,7 +651,7 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
         Piece nxt;
         bool has_next = false;
         int nxt_ids = -1;
-        mfma_piece<D, KV, QF32, APPEND>(a, cur, cur_ids, st, s_new, [&]() {
+        mfma_piece<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, st, s_new, [&]() {
             has_next = next_piece(nxt);
             if (has_next) nxt_ids = piece_ids(a, nxt, lane);  // in flight during this piece
         });

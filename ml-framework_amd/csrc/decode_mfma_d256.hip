@@ -4,9 +4,9 @@
 namespace pa {
 namespace {
 
-template <int D, int KV, bool QF32, bool APPEND>
+template <int D, int KV, bool QF32, bool APPEND, bool SHARED>
 void launch_one(DecodeArgs& a, int num_seqs, int64_t max_grid, hipStream_t s) {
-    auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND>;
+    auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND, SHARED>;
     // Resident workgroups per CU for this instance (queried once; read-only afterwards).
     constexpr int waves = decode_waves(D);
     static const int per_cu = [&] {
@@ -25,21 +25,25 @@ void launch_one(DecodeArgs& a, int num_seqs, int64_t max_grid, hipStream_t s) {
 }
 
 template <int KV, bool QF32>
-void pick_append(DecodeArgs& a, bool append, int num_seqs, int64_t max_grid, hipStream_t s) {
-    if (append) launch_one<256, KV, QF32, true>(a, num_seqs, max_grid, s);
-    else launch_one<256, KV, QF32, false>(a, num_seqs, max_grid, s);
+void pick(DecodeArgs& a, bool append, bool shared, int num_seqs, int64_t max_grid, hipStream_t s) {
+    if (shared) launch_one<256, KV, QF32, false, true>(a, num_seqs, max_grid, s);
+    else if (append) launch_one<256, KV, QF32, true, false>(a, num_seqs, max_grid, s);
+    else launch_one<256, KV, QF32, false, false>(a, num_seqs, max_grid, s);
 }
 
 }  // namespace
 
-void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, int num_seqs,
+void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
                             int64_t max_grid, hipStream_t s) {
     if (kv_dtype == PA_DTYPE_BF16) {
-        if (q_f32) pick_append<PA_DTYPE_BF16, true>(a, append, num_seqs, max_grid, s);
-        else pick_append<PA_DTYPE_BF16, false>(a, append, num_seqs, max_grid, s);
+        if (q_f32) pick<PA_DTYPE_BF16, true>(a, append, shared, num_seqs, max_grid, s);
+        else pick<PA_DTYPE_BF16, false>(a, append, shared, num_seqs, max_grid, s);
+    } else if (shared) {
+        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false, true>(a, num_seqs, max_grid, s);
+        else launch_one<256, PA_DTYPE_INT8, false, false, true>(a, num_seqs, max_grid, s);
     } else {  // int8 caches are appended by a separate launch before the decode
-        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false>(a, num_seqs, max_grid, s);
-        else launch_one<256, PA_DTYPE_INT8, false, false>(a, num_seqs, max_grid, s);
+        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false, false>(a, num_seqs, max_grid, s);
+        else launch_one<256, PA_DTYPE_INT8, false, false, false>(a, num_seqs, max_grid, s);
     }
 }
 

@@ -15,6 +15,7 @@
 // reduced across lanes with DPP, a partition-wide softmax in LDS, VALU P.V, and the same kind of
 // merge over fixed 256/512-token partitions (paged_decode_merge_kernel).
 #include <string>
+#include <vector>
 
 #include "append_int8.h"
 #include "decode_common.h"
@@ -276,9 +277,9 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
         append = false;  // the decode below reads the appended cache
     }
     switch (cfg->head_dim) {
-        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
-        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
-        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, append, num_seqs, max_grid, s); break;
+        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
     if (max_units > cfg->num_kv_heads) {  // more than one range: a row may span two
@@ -348,6 +349,193 @@ pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float*
     return decode_impl("pa_paged_decode_append", true, stream, cfg, out, q, k_new, v_new, k_cache, v_cache,
                        k_scale, v_scale, k_absmax, v_absmax, block_tables, context_lens, num_seqs,
                        max_blocks_per_seq, max_context_len, workspace, workspace_bytes);
+}
+
+}  // extern "C"
+
+// ---- shared-prefix decode ----
+//
+// Sequences forked from one parent keep the parent's first blocks in their tables (copy-on-write
+// sharing). pa_paged_decode reads those blocks once per sequence; this entry point reads them once
+// per group of up to 16 / G sequences: the group's query heads fill the 16 MFMA columns of one
+// pass over the shared blocks (a prefix row), each sequence's own blocks form a suffix row, and a
+// merge combines the two per sequence with the usual log-sum-exp reduction. The result is the same
+// attention as pa_paged_decode's over the whole context.
+
+namespace {
+
+// Groups the host-side link counts: shared_with_prev[s] = leading table entries sequence s has in
+// common with sequence s - 1 (entry 0 ignored). A run of linked sequences shares the minimum of
+// its links; runs are cut into groups of at most 16 / G members, and a group of one is no group.
+std::vector<int32_t> build_plan_host(int32_t num_seqs, int G, const int32_t* shared_with_prev, int32_t* num_groups) {
+    const int cap = 16 / G;
+    std::vector<int32_t> groups, seqinfo(static_cast<size_t>(num_seqs) * pa::kPlanSeqInts, 0);
+    for (int32_t s = 0; s < num_seqs; s++) seqinfo[static_cast<size_t>(s) * pa::kPlanSeqInts] = -1;
+    int32_t s = 0;
+    while (s < num_seqs) {
+        int32_t e = s + 1;  // run [s, e)
+        while (e < num_seqs && shared_with_prev[e] > 0) e++;
+        for (int32_t c0 = s; c0 < e; c0 += cap) {
+            const int32_t c1 = c0 + cap < e ? c0 + cap : e;
+            if (c1 - c0 < 2) continue;
+            int32_t shared = INT32_MAX;
+            for (int32_t t = c0 + 1; t < c1; t++) shared = shared_with_prev[t] < shared ? shared_with_prev[t] : shared;
+            const int32_t g = static_cast<int32_t>(groups.size() / pa::kPlanGroupInts);
+            groups.push_back(c0);
+            groups.push_back(c1 - c0);
+            groups.push_back(shared);
+            for (int32_t t = c0; t < c1; t++) {
+                seqinfo[static_cast<size_t>(t) * pa::kPlanSeqInts] = g;
+                seqinfo[static_cast<size_t>(t) * pa::kPlanSeqInts + 1] = shared;
+            }
+        }
+        s = e;
+    }
+    *num_groups = static_cast<int32_t>(groups.size() / pa::kPlanGroupInts);
+    groups.insert(groups.end(), seqinfo.begin(), seqinfo.end());
+    return groups;
+}
+
+size_t plan_bytes_for(int32_t num_seqs) {
+    return (static_cast<size_t>(num_seqs / 2) * pa::kPlanGroupInts + static_cast<size_t>(num_seqs) * pa::kPlanSeqInts) *
+           sizeof(int32_t);
+}
+
+// Slots of 16 rows: 2 per unit, then one per (row, KV head) of the decode's list (num_seqs +
+// num_groups rows, num_groups <= num_seqs / 2); and a block prefix over the rows.
+int64_t prefix_slots(const pa_config* cfg, int32_t num_seqs, int32_t max_len) {
+    return 2 * mfma_max_units(cfg, num_seqs, max_len, 0) +
+           (static_cast<int64_t>(num_seqs) + num_seqs / 2) * cfg->num_kv_heads;
+}
+size_t prefix_workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len) {
+    if (num_seqs <= 0) return 0;
+    const int64_t rows = prefix_slots(cfg, num_seqs, max_len) * pa::kPrefixSlotRows;
+    const int64_t prefs = static_cast<int64_t>(num_seqs) + num_seqs / 2 + 1;
+    return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float) + static_cast<size_t>(prefs) * 4;
+}
+
+}  // namespace
+
+extern "C" {
+
+pa_status pa_prefix_plan_bytes(int32_t num_seqs, size_t* bytes) {
+    if (!bytes || num_seqs < 0) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_prefix_plan_bytes: bad argument");
+    *bytes = plan_bytes_for(num_seqs);
+    return pa::clear_error();
+}
+
+pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t num_seqs,
+                               const int32_t* shared_with_prev, void* plan, size_t plan_bytes, int32_t* num_groups) {
+    const std::string f = "pa_prefix_plan_build";
+    pa_status st = pa::check_config(cfg, f.c_str());
+    if (st != PA_SUCCESS) return st;
+    if (num_seqs < 0 || !num_groups || (num_seqs > 0 && (!shared_with_prev || !plan)))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": bad argument");
+    const int G = cfg->num_q_heads / cfg->num_kv_heads;
+    if (G < 1 || G > 16) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": unsupported Hq / Hkv ratio");
+    if (plan_bytes < plan_bytes_for(num_seqs))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": plan buffer smaller than pa_prefix_plan_bytes");
+    *num_groups = 0;
+    if (num_seqs == 0) return pa::clear_error();
+    for (int32_t s = 1; s < num_seqs; s++)
+        if (shared_with_prev[s] < 0) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": negative shared count");
+    int32_t ng = 0;
+    const std::vector<int32_t> host = build_plan_host(num_seqs, G, shared_with_prev, &ng);
+    hipStream_t s = pa::native(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    PA_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": the stream is capturing a graph");
+    // The host vector dies with this call: the copy is waited for.
+    PA_HIP_CHECK(hipMemcpyAsync(plan, host.data(), host.size() * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    PA_HIP_CHECK(hipStreamSynchronize(s));
+    *num_groups = ng;
+    return pa::clear_error();
+}
+
+pa_status pa_prefix_workspace_size(const pa_config* cfg, int32_t num_seqs, int32_t max_context_len, size_t* bytes) {
+    pa_status st = pa::check_config(cfg, "pa_prefix_workspace_size");
+    if (st != PA_SUCCESS) return st;
+    if (!bytes || num_seqs < 0 || max_context_len < 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_prefix_workspace_size: bad argument");
+    *bytes = prefix_workspace_bytes_for(cfg, num_seqs, max_context_len);
+    return pa::clear_error();
+}
+
+pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                 const void* k_cache, const void* v_cache, const float* k_scale,
+                                 const float* v_scale, const int32_t* block_tables, const int32_t* context_lens,
+                                 int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
+                                 const void* plan, int32_t num_groups, void* workspace, size_t workspace_bytes) {
+    const std::string f = "pa_paged_decode_prefix";
+    pa_status st = pa::check_config(cfg, f.c_str());
+    if (st != PA_SUCCESS) return st;
+    if (num_seqs < 0 || max_blocks_per_seq < 0 || max_context_len < 0 || num_groups < 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": negative size");
+    if (num_seqs == 0) return pa::clear_error();
+    if (cfg->kv_dtype == PA_DTYPE_FP32)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": bf16 or int8 caches only");
+    if (num_groups > num_seqs / 2) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": more groups than pairs");
+    if (num_seqs + num_groups > pa::kMaxPersistentSeqs - 1)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": num_seqs + num_groups above " +
+                                                       std::to_string(pa::kMaxPersistentSeqs - 1));
+    if (!out || !q || !k_cache || !v_cache || !block_tables || !context_lens || !plan)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": null pointer");
+    if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": int8 cache needs k_scale and v_scale");
+    const int G = cfg->num_q_heads / cfg->num_kv_heads;
+    if (!(G == 1 || G == 2 || G == 4 || G == 8 || G == 16))
+        return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": unsupported Hq / Hkv ratio");
+    if (cfg->num_kv_heads > 65535) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": too many KV heads");
+    const int32_t max_len = effective_max_len(max_context_len, max_blocks_per_seq);
+    const size_t need = prefix_workspace_bytes_for(cfg, num_seqs, max_len);
+    if (!workspace || workspace_bytes < need)
+        return pa::set_error(PA_ERROR_WORKSPACE_TOO_SMALL,
+                             f + ": workspace of " + std::to_string(need) + " bytes required");
+    pa::DecodeArgs a{};
+    a.out = out;
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.block_tables = block_tables;
+    a.context_lens = context_lens;
+    a.num_kv_heads = cfg->num_kv_heads;
+    a.group = G;
+    a.max_blocks_per_seq = max_blocks_per_seq;
+    a.num_blocks = cfg->num_blocks;
+    a.max_context_len = max_len;
+    a.max_parts = 1;
+    a.split_blocks = 0;  // equal ranges per worker (partition_size does not apply here)
+    a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
+    a.scale = pa::resolve_scale(cfg);
+    a.plan = static_cast<const int32_t*>(plan);
+    a.num_groups = num_groups;
+    const int64_t max_units = mfma_max_units(cfg, num_seqs, max_len, 0);
+    const int64_t rows = prefix_slots(cfg, num_seqs, max_len) * pa::kPrefixSlotRows;
+    a.row_slot_base = static_cast<int32_t>(2 * max_units);
+    a.ws_o = static_cast<float*>(workspace);
+    a.ws_m = a.ws_o + rows * cfg->head_dim;
+    a.ws_l = a.ws_m + rows;
+    a.ws_pref = reinterpret_cast<int32_t*>(a.ws_l + rows);
+    hipStream_t s = pa::native(stream);
+    const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
+    const int64_t max_grid = max_units > 0 ? max_units : 1;
+    switch (cfg->head_dim) {
+        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+    }
+    PA_HIP_CHECK(hipGetLastError());
+    dim3 mgrid(cfg->num_kv_heads, num_seqs);
+    switch (cfg->head_dim) {
+        case 64: pa::paged_decode_merge_prefix_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+        case 128: pa::paged_decode_merge_prefix_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+        default: pa::paged_decode_merge_prefix_kernel<256><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+    }
+    PA_HIP_CHECK(hipGetLastError());
+    return pa::clear_error();
 }
 
 }  // extern "C"

@@ -56,6 +56,7 @@ EXPORTS = (
     "pa_block_bytes", "pa_copy_blocks", "pa_gather_blocks", "pa_scatter_blocks", "pa_read_block_f32",
     "pa_write_block_f32",
     "pa_qkv_workspace_size", "pa_qkv_project_append", "pa_o_workspace_size", "pa_o_project",
+    "pa_prefix_plan_bytes", "pa_prefix_plan_build", "pa_prefix_workspace_size", "pa_paged_decode_prefix",
 )
 
 
@@ -141,6 +142,10 @@ _SIGNATURES = {
     "pa_paged_decode_append": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                _P, _SZ],
     "pa_chunked_prefill": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
+    "pa_prefix_plan_bytes": [_I32, ctypes.POINTER(_SZ)],
+    "pa_prefix_plan_build": [_P, _CFG, _I32, _P, _P, _SZ, ctypes.POINTER(_I32)],
+    "pa_prefix_workspace_size": [_CFG, _I32, _I32, ctypes.POINTER(_SZ)],
+    "pa_paged_decode_prefix": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _I32, _P, _SZ],
     "pa_block_bytes": [_CFG, ctypes.POINTER(_SZ)],
     "pa_copy_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32],
     "pa_gather_blocks": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _I32, _P],
@@ -338,6 +343,38 @@ def paged_decode_append(stream, cfg: PaConfig, out, q, k_new, v_new, k_cache, v_
          _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
          _ptr(k_absmax), _ptr(v_absmax), _ptr(block_tables), _ptr(context_lens), num_seqs,
          max_blocks_per_seq, max_context_len, _ptr(workspace), workspace_bytes)
+
+
+def prefix_plan_bytes(num_seqs: int) -> int:
+    out = ctypes.c_size_t()
+    call("pa_prefix_plan_bytes", num_seqs, ctypes.byref(out))
+    return out.value
+
+
+def prefix_plan_build(stream, cfg: PaConfig, shared_with_prev, plan, plan_bytes) -> int:
+    """shared_with_prev: host int32 sequence (leading table entries sequence s shares with s - 1).
+    Writes the device plan and returns the group count for paged_decode_prefix."""
+    import numpy as np
+    links = np.ascontiguousarray(np.asarray(shared_with_prev, dtype=np.int32))
+    ng = ctypes.c_int32()
+    call("pa_prefix_plan_build", stream.handle if stream else None, ctypes.byref(cfg), int(links.size),
+         links.ctypes.data_as(ctypes.c_void_p), _ptr(plan), plan_bytes, ctypes.byref(ng))
+    return ng.value
+
+
+def prefix_workspace_size(cfg: PaConfig, num_seqs: int, max_context_len: int) -> int:
+    out = ctypes.c_size_t()
+    call("pa_prefix_workspace_size", ctypes.byref(cfg), num_seqs, max_context_len, ctypes.byref(out))
+    return out.value
+
+
+def paged_decode_prefix(stream, cfg: PaConfig, out, q, k_cache, v_cache, k_scale, v_scale, block_tables,
+                        context_lens, num_seqs, max_blocks_per_seq, max_context_len, plan, num_groups,
+                        workspace, workspace_bytes):
+    call("pa_paged_decode_prefix", stream.handle if stream else None, ctypes.byref(cfg), _ptr(out), _ptr(q),
+         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_tables),
+         _ptr(context_lens), num_seqs, max_blocks_per_seq, max_context_len, _ptr(plan), num_groups,
+         _ptr(workspace), workspace_bytes)
 
 
 def chunked_prefill(stream, cfg: PaConfig, out, q, q_start_loc, prefix_lens, k_cache, v_cache,
