@@ -471,6 +471,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 measurements")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time the C3 chunked prefill call only and print its own JSON line: for profiling")
+    ap.add_argument("--only-c5", action="store_true",
+                    help="time C5 through pa_paged_decode and pa_paged_decode_prefix and print their JSON line")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run 10 plain device-to-device copies of this many MiB through pa_memcpy, the "
                          "reference kernel for scaling hardware byte counters")
@@ -501,6 +503,13 @@ def main():
         flops = float(4 * w3.num_q_heads * w3.head_dim * np.sum(P * L + L * (L + 1) / 2))
         print(json.dumps({"mode": "only-prefill", "workload": "C3 chunked prefill", "us": round(ms * 1e3, 3),
                           "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "steps": args.steps}), flush=True)
+        return
+    if args.only_c5:
+        w5 = wl.make_c5()
+        plain = run_decode_config(w5, timer, stream, args.steps, args.warmup, False, 5)
+        shared = run_prefix_decode(w5, timer, stream, args.steps, args.warmup, 5)
+        print(json.dumps({"mode": "only-c5", "workload": "C5 decode", "pa_paged_decode": plain,
+                          "pa_paged_decode_prefix": shared, "steps": args.steps}), flush=True)
         return
     cfg = config_of(w, args.partition_size)
     S = w.num_seqs
