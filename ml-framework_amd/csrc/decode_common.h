@@ -156,16 +156,10 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
             const int64_t pi = pidx_of(p0 + (ok ? lane : 0), g);
             const float pm = ok ? a.ws_m[pi] : -INFINITY;
             const float pl = ok ? a.ws_l[pi] : 0.0f;
-            const float cm = fmaxf(M, wave_max(pm));  // finite: every partial saw a token
-            const float r = __expf(M - cm);           // rescale of earlier rounds (0 on the first)
-            const float w = ok ? __expf(pm - cm) : 0.0f;
-            L = L * r + wave_sum(pl * w);
-#pragma unroll
-            for (int k = 0; k < DPL; k++) o[k] *= r;
-            for (int u = 0; u < cnt; u += UNROLL) {
-                // Every load of a batch is issued before any is used; past cnt (uniform) nothing
-                // is loaded and the weight read is lane 63's or beyond-cnt zero, times zero.
-                float x[UNROLL][DPL];
+            // Every load of a batch is issued before any is used; past cnt (uniform) nothing is
+            // loaded and the weight read is lane 63's or beyond-cnt zero, times zero.
+            float x[UNROLL][DPL];
+            auto load_batch = [&](int u) {
 #pragma unroll
                 for (int j = 0; j < UNROLL; j++) {
                     if (u + j < cnt) {
@@ -177,6 +171,16 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
                         for (int k = 0; k < DPL; k++) x[j][k] = 0.0f;
                     }
                 }
+            };
+            load_batch(0);  // needs the slot indices only: in flight with the (max, sum) loads
+            const float cm = fmaxf(M, wave_max(pm));  // finite: every partial saw a token
+            const float r = __expf(M - cm);           // rescale of earlier rounds (0 on the first)
+            const float w = ok ? __expf(pm - cm) : 0.0f;
+            L = L * r + wave_sum(pl * w);
+#pragma unroll
+            for (int k = 0; k < DPL; k++) o[k] *= r;
+            for (int u = 0; u < cnt; u += UNROLL) {
+                if (u > 0) load_batch(u);
 #pragma unroll
                 for (int j = 0; j < UNROLL; j++) {
                     const float wj = readlane_f(w, min(u + j, 63));
