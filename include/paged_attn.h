@@ -273,6 +273,13 @@ pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t 
                                const int32_t* shared_with_prev, void* plan, size_t plan_bytes,
                                int32_t* num_groups);
 
+/* The same plan written to host memory (plan_host, plan_bytes >= pa_prefix_plan_bytes), for a
+ * caller that uploads it itself: int32 records {first sequence, members, shared blocks} for each
+ * of the *num_groups groups, then {group or -1, shared blocks or 0} for each sequence. No GPU
+ * call. */
+pa_status pa_prefix_plan_fill(const pa_config* cfg, int32_t num_seqs, const int32_t* shared_with_prev,
+                              int32_t* plan_host, size_t plan_bytes, int32_t* num_groups);
+
 /* Workspace of pa_paged_decode_prefix for up to num_seqs sequences of up to max_context_len. */
 pa_status pa_prefix_workspace_size(const pa_config* cfg, int32_t num_seqs, int32_t max_context_len,
                                    size_t* bytes);

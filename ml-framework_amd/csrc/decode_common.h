@@ -257,19 +257,22 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_prefix_kernel(const DecodeArgs a, int32_t num_seqs) {
     const int kvh = blockIdx.x, seq = blockIdx.y;
-    if (clamp_len(a, a.context_lens[seq]) <= 0) return;  // zero output, written by the decode
     const int NG = a.num_groups;
     const int Hkv = a.num_kv_heads, G = a.group;
     const int32_t* groups = a.plan;
     const int32_t* seqinfo = a.plan + static_cast<int64_t>(NG) * kPlanGroupInts;
-    int grp = seqinfo[static_cast<int64_t>(seq) * kPlanSeqInts];
-    if (grp >= NG) grp = -1;
     const int row = NG + seq;
+    // Independent loads first (a test between them would serialise their round trips).
+    const int raw_len = a.context_lens[seq];
+    int grp = seqinfo[static_cast<int64_t>(seq) * kPlanSeqInts];
     const int64_t total = a.ws_pref[NG + num_seqs];
-    const int64_t C = split_range_blocks(a, total);
     const int64_t R0 = a.ws_pref[row];
-    const int nbr = a.ws_pref[row + 1] - a.ws_pref[row];
-    if (R0 < 0 || nbr < 0 || R0 + nbr > total) return;  // a prefix table that does not fit the slots
+    const int64_t R1 = a.ws_pref[row + 1];
+    if (clamp_len(a, raw_len) <= 0) return;  // zero output, written by the decode
+    if (grp >= NG) grp = -1;
+    const int64_t C = split_range_blocks(a, total);
+    const int nbr = static_cast<int>(R1 - R0);
+    if (R0 < 0 || nbr < 0 || R1 > total) return;  // a prefix table that does not fit the slots
     int ns = 0;
     int64_t w1 = 0;
     bool s_inside = false;

@@ -14,6 +14,7 @@
 // fp32 caches (decode_fp32.h): one workgroup per (partition, KV head, sequence), VALU dot products
 // reduced across lanes with DPP, a partition-wide softmax in LDS, VALU P.V, and the same kind of
 // merge over fixed 256/512-token partitions (paged_decode_merge_kernel).
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -424,12 +425,12 @@ pa_status pa_prefix_plan_bytes(int32_t num_seqs, size_t* bytes) {
     return pa::clear_error();
 }
 
-pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t num_seqs,
-                               const int32_t* shared_with_prev, void* plan, size_t plan_bytes, int32_t* num_groups) {
-    const std::string f = "pa_prefix_plan_build";
+pa_status pa_prefix_plan_fill(const pa_config* cfg, int32_t num_seqs, const int32_t* shared_with_prev,
+                              int32_t* plan_host, size_t plan_bytes, int32_t* num_groups) {
+    const std::string f = "pa_prefix_plan_fill";
     pa_status st = pa::check_config(cfg, f.c_str());
     if (st != PA_SUCCESS) return st;
-    if (num_seqs < 0 || !num_groups || (num_seqs > 0 && (!shared_with_prev || !plan)))
+    if (num_seqs < 0 || !num_groups || (num_seqs > 0 && (!shared_with_prev || !plan_host)))
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": bad argument");
     const int G = cfg->num_q_heads / cfg->num_kv_heads;
     if (G < 1 || G > 16) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": unsupported Hq / Hkv ratio");
@@ -441,6 +442,23 @@ pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t 
         if (shared_with_prev[s] < 0) return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": negative shared count");
     int32_t ng = 0;
     const std::vector<int32_t> host = build_plan_host(num_seqs, G, shared_with_prev, &ng);
+    std::copy(host.begin(), host.end(), plan_host);
+    *num_groups = ng;
+    return pa::clear_error();
+}
+
+pa_status pa_prefix_plan_build(pa_stream* stream, const pa_config* cfg, int32_t num_seqs,
+                               const int32_t* shared_with_prev, void* plan, size_t plan_bytes, int32_t* num_groups) {
+    const std::string f = "pa_prefix_plan_build";
+    if (num_seqs < 0 || !num_groups || (num_seqs > 0 && !plan))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": bad argument");
+    *num_groups = 0;
+    std::vector<int32_t> host(plan_bytes_for(num_seqs) / sizeof(int32_t) + 1);
+    int32_t ng = 0;
+    pa_status st = pa_prefix_plan_fill(cfg, num_seqs, shared_with_prev, host.data(), plan_bytes, &ng);
+    if (st != PA_SUCCESS) return st;
+    if (num_seqs == 0) return pa::clear_error();
+    host.resize(static_cast<size_t>(ng) * pa::kPlanGroupInts + static_cast<size_t>(num_seqs) * pa::kPlanSeqInts);
     hipStream_t s = pa::native(stream);
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     PA_HIP_CHECK(hipStreamIsCapturing(s, &cs));

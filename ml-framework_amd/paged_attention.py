@@ -56,7 +56,8 @@ EXPORTS = (
     "pa_block_bytes", "pa_copy_blocks", "pa_gather_blocks", "pa_scatter_blocks", "pa_read_block_f32",
     "pa_write_block_f32",
     "pa_qkv_workspace_size", "pa_qkv_project_append", "pa_o_workspace_size", "pa_o_project",
-    "pa_prefix_plan_bytes", "pa_prefix_plan_build", "pa_prefix_workspace_size", "pa_paged_decode_prefix",
+    "pa_prefix_plan_bytes", "pa_prefix_plan_build", "pa_prefix_plan_fill", "pa_prefix_workspace_size",
+    "pa_paged_decode_prefix",
 )
 
 
@@ -144,6 +145,7 @@ _SIGNATURES = {
     "pa_chunked_prefill": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
     "pa_prefix_plan_bytes": [_I32, ctypes.POINTER(_SZ)],
     "pa_prefix_plan_build": [_P, _CFG, _I32, _P, _P, _SZ, ctypes.POINTER(_I32)],
+    "pa_prefix_plan_fill": [_CFG, _I32, _P, _P, _SZ, ctypes.POINTER(_I32)],
     "pa_prefix_workspace_size": [_CFG, _I32, _I32, ctypes.POINTER(_SZ)],
     "pa_paged_decode_prefix": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _I32, _P, _SZ],
     "pa_block_bytes": [_CFG, ctypes.POINTER(_SZ)],
@@ -360,6 +362,20 @@ def prefix_plan_build(stream, cfg: PaConfig, shared_with_prev, plan, plan_bytes)
     call("pa_prefix_plan_build", stream.handle if stream else None, ctypes.byref(cfg), int(links.size),
          links.ctypes.data_as(ctypes.c_void_p), _ptr(plan), plan_bytes, ctypes.byref(ng))
     return ng.value
+
+
+def prefix_plan_fill(cfg: PaConfig, shared_with_prev):
+    """Host-side plan (no GPU): returns (groups int32 [G][3], seqinfo int32 [S][2])."""
+    import numpy as np
+    links = np.ascontiguousarray(np.asarray(shared_with_prev, dtype=np.int32))
+    S = int(links.size)
+    nbytes = prefix_plan_bytes(S)
+    buf = np.zeros(max(nbytes // 4, 1), np.int32)
+    ng = ctypes.c_int32()
+    call("pa_prefix_plan_fill", ctypes.byref(cfg), S, links.ctypes.data_as(ctypes.c_void_p),
+         buf.ctypes.data_as(ctypes.c_void_p), nbytes, ctypes.byref(ng))
+    g = ng.value
+    return buf[:3 * g].reshape(g, 3).copy(), buf[3 * g:3 * g + 2 * S].reshape(S, 2).copy()
 
 
 def prefix_workspace_size(cfg: PaConfig, num_seqs: int, max_context_len: int) -> int:

@@ -175,3 +175,54 @@ def test_prefix_plan_and_args_validated_on_the_host(stream):
     with pytest.raises(pa.PagedAttentionError):  # more groups than pairs of sequences
         pa.paged_decode_prefix(stream, cfg, dummy, dummy, dummy, dummy, None, None, dummy, dummy, 4, 4, 64,
                                plan, 3, dummy, 1 << 20)
+
+
+def test_prefix_decode_graph_replay_matches_eager():
+    """The shared-prefix decode records kernels only: captured once, replayed with new queries,
+    every replay equals the eager call bit for bit and the oracle within tolerance."""
+    import torch
+
+    torch.cuda.init()
+    dev = pa.Device(0)
+    gs = pa.Stream(dev)  # a library stream: the null stream cannot capture
+    try:
+        rng = np.random.default_rng(77)
+        lens = rng.integers(300, 600, size=9).astype(np.int32)
+        w, links = shared_case(78, lens, [(0, 4, 10), (4, 5, 6)], Hq=32, Hkv=8, D=128)
+        inp = wl.numpy_inputs(w, 9)
+        cfg = config_for(w)
+        S = w.num_seqs
+        pb = pa.prefix_plan_bytes(S)
+        plan = empty_gpu((pb,), np.uint8)
+        torch.cuda.synchronize()
+        ng = pa.prefix_plan_build(gs, cfg, links, plan, pb)
+        wsb = pa.prefix_workspace_size(cfg, S, w.max_context_len)
+        ws = empty_gpu((wsb,), np.uint8)
+        out = empty_gpu((S, w.num_q_heads, w.head_dim), np.float32)
+        q = to_gpu(inp["q"])
+        kc, vc = to_gpu(inp["k_cache"]), to_gpu(inp["v_cache"])
+        args = (q, kc, vc, None, None, to_gpu(w.block_tables), to_gpu(w.context_lens), S, w.max_blocks,
+                w.max_context_len, plan, ng, ws, wsb)
+        torch.cuda.synchronize()
+        g = pa.Graph().capture(gs)
+        pa.paged_decode_prefix(gs, cfg, out, *args)
+        g.end()
+        try:
+            for r in range(3):
+                qv = orc.bf16_from_f32(rng.standard_normal(inp["q"].shape, dtype=np.float32))
+                q.copy_(to_gpu(qv))
+                torch.cuda.synchronize()
+                g.launch(gs)
+                gs.synchronize()
+                replay = to_np(out).copy()
+                pa.paged_decode_prefix(gs, cfg, out, *args)
+                gs.synchronize()
+                np.testing.assert_array_equal(replay, to_np(out))
+                ref = orc.paged_decode(cfg, qv, inp["k_cache"], inp["v_cache"], None, None, w.block_tables,
+                                       w.context_lens, n_threads=NTHREADS)
+                check_close(replay, ref, **tol_for(1), what=f"graph replay {r}")
+        finally:
+            g.destroy()
+    finally:
+        gs.destroy()
+        dev.close()
