@@ -132,68 +132,115 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Log-sum-exp merge of the partials of one (sequence, KV head): wave w takes query heads
-// w, w + 4, ...; per head, lane j loads partial j's (max, sum) (64 partials per round), the wave
-// reduces them to the round's max and weighted sum, and the outputs (lane l: dims l, l + 64, ..)
-// are loaded 16 partials at a time, each weighted by the value its lane computed. pidx_of(u, g) is
-// the workspace row of partial u of head g of the group.
+// Log-sum-exp merge of split partials. Partials [pbeg, pend) of head g merged into (M, L, o) (this lane's dims lane, lane + 64, ..):
+// lane j loads partial j's (max, sum), 64 partials per round, the wave reduces them to the round's
+// max and weighted sum, and the outputs are loaded UNROLL partials at a time, each weighted by the
+// value its lane computed. An empty range leaves M = -inf, L = 0, o = 0.
 template <int D, typename PidxOf>
-__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
+__device__ __forceinline__ void merge_range(const DecodeArgs& a, int g, int pbeg, int pend, PidxOf pidx_of, float& M,
+                                            float& L, float (&o)[D / 64]) {
     constexpr int DPL = D / 64;  // dims per lane
     constexpr int UNROLL = 16;   // partials whose output loads are issued together
+    const int lane = threadIdx.x & 63;
+    M = -INFINITY;
+    L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DPL; k++) o[k] = 0.0f;
+    for (int p0 = pbeg; p0 < pend; p0 += 64) {
+        const int cnt = min(64, pend - p0);
+        const bool ok = lane < cnt;
+        const int64_t pi = pidx_of(p0 + (ok ? lane : 0), g);
+        const float pm = ok ? a.ws_m[pi] : -INFINITY;
+        const float pl = ok ? a.ws_l[pi] : 0.0f;
+        // Every load of a batch is issued before any is used; past cnt (uniform) nothing is
+        // loaded and the weight read is lane 63's or beyond-cnt zero, times zero.
+        float x[UNROLL][DPL];
+        auto load_batch = [&](int u) {
+#pragma unroll
+            for (int j = 0; j < UNROLL; j++) {
+                if (u + j < cnt) {
+                    const int64_t pj = pidx_of(p0 + u + j, g);
+#pragma unroll
+                    for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < DPL; k++) x[j][k] = 0.0f;
+                }
+            }
+        };
+        load_batch(0);  // needs the slot indices only: in flight with the (max, sum) loads
+        const float cm = fmaxf(M, wave_max(pm));  // finite: every partial saw a token
+        const float r = __expf(M - cm);           // rescale of earlier rounds (0 on the first)
+        const float w = ok ? __expf(pm - cm) : 0.0f;
+        L = L * r + wave_sum(pl * w);
+#pragma unroll
+        for (int k = 0; k < DPL; k++) o[k] *= r;
+        for (int u = 0; u < cnt; u += UNROLL) {
+            if (u > 0) load_batch(u);
+#pragma unroll
+            for (int j = 0; j < UNROLL; j++) {
+                const float wj = readlane_f(w, min(u + j, 63));
+#pragma unroll
+                for (int k = 0; k < DPL; k++) o[k] += x[j][k] * wj;
+            }
+        }
+        M = cm;
+    }
+}
+
+// Merge of the nparts partials of (sequence, KV head): wave w takes heads w, w + 4, ... of the
+// group. pidx_of(u, g) is the workspace row of partial u of head g of the group.
+template <int D, typename PidxOf>
+__device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
+    constexpr int DPL = D / 64;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = a.group;
     for (int g = wave; g < G; g += 4) {
         const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * G + kvh * G + g;
-        float M = -INFINITY, L = 0.0f;
-        float o[DPL];
-#pragma unroll
-        for (int k = 0; k < DPL; k++) o[k] = 0.0f;
-        for (int p0 = 0; p0 < nparts; p0 += 64) {
-            const int cnt = min(64, nparts - p0);
-            const bool ok = lane < cnt;
-            const int64_t pi = pidx_of(p0 + (ok ? lane : 0), g);
-            const float pm = ok ? a.ws_m[pi] : -INFINITY;
-            const float pl = ok ? a.ws_l[pi] : 0.0f;
-            // Every load of a batch is issued before any is used; past cnt (uniform) nothing is
-            // loaded and the weight read is lane 63's or beyond-cnt zero, times zero.
-            float x[UNROLL][DPL];
-            auto load_batch = [&](int u) {
-#pragma unroll
-                for (int j = 0; j < UNROLL; j++) {
-                    if (u + j < cnt) {
-                        const int64_t pj = pidx_of(p0 + u + j, g);
-#pragma unroll
-                        for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < DPL; k++) x[j][k] = 0.0f;
-                    }
-                }
-            };
-            load_batch(0);  // needs the slot indices only: in flight with the (max, sum) loads
-            const float cm = fmaxf(M, wave_max(pm));  // finite: every partial saw a token
-            const float r = __expf(M - cm);           // rescale of earlier rounds (0 on the first)
-            const float w = ok ? __expf(pm - cm) : 0.0f;
-            L = L * r + wave_sum(pl * w);
-#pragma unroll
-            for (int k = 0; k < DPL; k++) o[k] *= r;
-            for (int u = 0; u < cnt; u += UNROLL) {
-                if (u > 0) load_batch(u);
-#pragma unroll
-                for (int j = 0; j < UNROLL; j++) {
-                    const float wj = readlane_f(w, min(u + j, 63));
-#pragma unroll
-                    for (int k = 0; k < DPL; k++) o[k] += x[j][k] * wj;
-                }
-            }
-            M = cm;
-        }
+        float M, L, o[DPL];
+        merge_range<D>(a, g, 0, nparts, pidx_of, M, L, o);
         const float inv = 1.0f / L;
 #pragma unroll
         for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
     }
+}
+
+// Merge of the nparts partials of one head g of (sequence, KV head) by the 4 waves of the
+// workgroup: wave w merges a quarter of the partials, and wave 0 combines the four states.
+template <int D, typename PidxOf>
+__device__ __forceinline__ void merge_head_wide(const DecodeArgs& a, int seq, int kvh, int g, int nparts,
+                                                PidxOf pidx_of) {
+    constexpr int DPL = D / 64;
+    __shared__ float s_m[4], s_l[4], s_o[4][D];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = (nparts + 3) / 4;
+    float M, L, o[DPL];
+    merge_range<D>(a, g, min(wave * q, nparts), min((wave + 1) * q, nparts), pidx_of, M, L, o);
+    if (lane == 0) {
+        s_m[wave] = M;
+        s_l[wave] = L;
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; k++) s_o[wave][lane + 64 * k] = o[k];
+    __syncthreads();
+    if (wave != 0) return;
+    float cm = s_m[0];  // finite: wave 0's quarter is never empty
+    for (int w = 1; w < 4; w++) cm = fmaxf(cm, s_m[w]);
+    float lt = 0.0f, ot[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; k++) ot[k] = 0.0f;
+    for (int w = 0; w < 4; w++) {
+        const float f = __expf(s_m[w] - cm);  // 0 for an empty quarter (-inf)
+        lt += s_l[w] * f;
+#pragma unroll
+        for (int k = 0; k < DPL; k++) ot[k] += s_o[w][lane + 64 * k] * f;
+    }
+    const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * a.group + kvh * a.group + g;
+    const float inv = 1.0f / lt;
+#pragma unroll
+    for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = ot[k] * inv;
 }
 
 // Merge pass: one workgroup per (KV head, sequence).
@@ -247,7 +294,8 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
     });
 }
 
-// Shared-prefix decode merge: one workgroup per (KV head, sequence). Rows of the decode's list
+// Shared-prefix decode merge: one workgroup per (KV head, sequence, query head of the group), its
+// 4 waves sharing the head's partials (a sequence's partials are many here). Rows of the decode's list
 // are the num_groups prefix rows, then one suffix row per sequence (its blocks after the shared
 // ones); every row's partials sit in 16-wide slots (slot 2u + {0, 1} of unit u, as above, or the
 // row's own slot row_slot_base + r * Hkv + kvh when the row lies inside one range). A
@@ -299,7 +347,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_prefix_kernel(const De
     if (grp < 0 && ns <= 1) return;  // written whole by the decode kernel
     if (ns + np == 0) return;
     // A row inside one range left its partial in its row slot, a split row one per range.
-    merge_partitions<D>(a, seq, kvh, ns + np, [&](int u, int g) -> int64_t {
+    merge_head_wide<D>(a, seq, kvh, static_cast<int>(blockIdx.z), ns + np, [&](int u, int g) -> int64_t {
         if (u < ns) {
             if (ns == 1) return (a.row_slot_base + static_cast<int64_t>(row) * Hkv + kvh) * kPrefixSlotRows + g;
             const int64_t unit = (w1 + u) * Hkv + kvh;

@@ -546,7 +546,7 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
         default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
-    dim3 mgrid(cfg->num_kv_heads, num_seqs);
+    dim3 mgrid(cfg->num_kv_heads, num_seqs, G);
     switch (cfg->head_dim) {
         case 64: pa::paged_decode_merge_prefix_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
         case 128: pa::paged_decode_merge_prefix_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
