@@ -226,3 +226,49 @@ def test_prefix_decode_graph_replay_matches_eager():
     finally:
         gs.destroy()
         dev.close()
+
+
+def test_c5_full_size_split_and_prefix_agree(stream):
+    """Full C5 (8 sequences of 16-32k tokens, 512 shared blocks): the default split, a 64-token
+    split (about 500 partials per row: the merge's multi-round path) and the shared-prefix decode
+    compute the same attention in different orders and agree within the bf16 tolerance."""
+    import torch
+
+    w = wl.make_c5()
+    S, Hq, Hkv, D = w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(55)
+
+    def bf16(*shape):
+        x = torch.randn(*shape, generator=g, device="cuda:0", dtype=torch.float32)
+        return (x.view(torch.int32) >> 16).to(torch.int16)
+
+    q = bf16(S, Hq, D)
+    kc, vc = bf16(w.num_blocks, Hkv, 16, D), bf16(w.num_blocks, Hkv, 16, D)
+    tables, lens = to_gpu(w.block_tables), to_gpu(w.context_lens)
+    mcl = w.max_context_len
+    outs = {}
+    for name, part in (("default", 0), ("p64", 64)):
+        cfg = config_for(w, partition_size=part)
+        wsb = pa.decode_workspace_size(cfg, S, mcl)
+        ws = empty_gpu((wsb,), np.uint8)
+        out = empty_gpu((S, Hq, D), np.float32)
+        pa.paged_decode(stream, cfg, out, q, kc, vc, None, None, tables, lens, S, w.max_blocks, mcl, ws, wsb)
+        _sync()
+        outs[name] = to_np(out).copy()
+    cfg = config_for(w)
+    links = np.zeros(S, np.int32)
+    links[1:] = w.shared_prefix_blocks
+    pb = pa.prefix_plan_bytes(S)
+    plan = empty_gpu((pb,), np.uint8)
+    ng = pa.prefix_plan_build(stream, cfg, links, plan, pb)
+    assert ng == 2
+    wsb = pa.prefix_workspace_size(cfg, S, mcl)
+    ws = empty_gpu((wsb,), np.uint8)
+    out = empty_gpu((S, Hq, D), np.float32)
+    pa.paged_decode_prefix(stream, cfg, out, q, kc, vc, None, None, tables, lens, S, w.max_blocks, mcl, plan, ng,
+                           ws, wsb)
+    _sync()
+    outs["prefix"] = to_np(out).copy()
+    check_close(outs["p64"], outs["default"], **tol_for(1), what="C5 64-token split vs default")
+    check_close(outs["prefix"], outs["default"], **tol_for(1), what="C5 shared-prefix vs default")
