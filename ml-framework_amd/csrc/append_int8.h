@@ -1,13 +1,18 @@
-// append_int8.h -- the quantising append of one segment into an int8 paged cache, shared by
-// pa_kv_append and the last-token append of pa_paged_decode_append.
+// append_int8.h -- the quantising append into an int8 paged cache, shared by pa_kv_append, the
+// last-token append of pa_paged_decode_append and pa_write_block_f32.
 //
 // Policy (the reference's QuantizeSymmetric / Dequantize, Quantization/Operations/
 // QuantizationOperations.cs:188-200, applied per (block, KV head) with a running absmax): a
-// segment is a run of consecutive tokens of the call that land in the same block; its first
-// token's wave owns that (block, head) for the call. Writing row 0 starts the block afresh
-// (scale = segment absmax / 127); otherwise a segment whose absmax exceeds the block's grows the
-// scale and requantises every row it does not overwrite; the new rows are quantised with the
+// segment is a maximal run of consecutive tokens of the call whose slots are valid and lie in one
+// block. Segments are applied in call order. Writing row 0 starts the block afresh (scale =
+// segment absmax / 127); otherwise a segment whose absmax exceeds the block's grows the scale and
+// requantises every row it does not overwrite; the segment's rows are then quantised with the
 // block's (possibly grown) scale.
+//
+// Ownership: one workgroup per token of the call; the workgroup of the first token of the call
+// that lands in a block owns that block and applies every segment of it, in call order, one wave
+// per (KV head, K|V). A block's tokens may therefore arrive in any order, split by invalid slots
+// or by other blocks' tokens, without two workgroups touching one block.
 #pragma once
 
 #include "pa_internal.h"
@@ -18,43 +23,34 @@ __device__ __forceinline__ float load_act(const void* p, bool bf16, int64_t i) {
     return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
-// Wave (64 lanes) for token i of the call, KV head h, K (is_v false) or V. slot_at(t) is the slot
-// of token t (out of [0, capacity): skipped); src holds the tokens' values in the activation dtype,
-// token t's (head h, dim d) at t * tok_stride + h * D + d. The tile of (block, h) is K [16][D] or
-// V [D][16] in `cache`.
+// One segment [s, e) of block blk for KV head h, K (is_v false) or V, applied by one wave (64
+// lanes; lane l owns dims l, l + 64, ..). slot_at(t) is token t's slot; src holds the tokens'
+// values in the activation dtype, token t's (head h, dim d) at t * tok_stride + h * D + d. The
+// tile of (blk, h) is K [16][D] or V [D][16] in `cache`. (amax, cur_scale) carry the block's
+// statistics from one segment of this (block, head) to the next: have_stats false loads them.
 template <int D, typename SlotAt>
-__device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf16, int64_t tok_stride, SlotAt slot_at,
-                                                    int32_t i,
-                                                    int32_t n_tok, int8_t* cache, float* scale, float* absmax,
-                                                    int h, int32_t num_kv_heads, int64_t capacity, bool is_v) {
+__device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16, int64_t tok_stride, SlotAt slot_at,
+                                                  int32_t s, int32_t e, int64_t blk, int8_t* cache, float* scale,
+                                                  float* absmax, int h, int32_t num_kv_heads, bool is_v, float& amax,
+                                                  float& cur_scale, bool& have_stats) {
 #pragma clang fp contract(off)
+    static_assert(D % 64 == 0, "int8 caches take head_dim 64, 128 or 256");
     constexpr int kPer = D / 64;  // elements per lane
     const int lane = threadIdx.x & 63;
-    const int64_t slot = slot_at(i);
-    if (slot < 0 || slot >= capacity) return;
-    const int64_t blk = slot / kBlockSize;
-    if (i > 0) {
-        const int64_t prev = slot_at(i - 1);
-        if (prev >= 0 && prev < capacity && prev / kBlockSize == blk) return;  // not a segment head
-    }
-    // Extent of the segment, the slots it writes and the absmax of its values for head h.
-    int end = i;
+    // Rows the segment writes (lane j looks at tokens s + j, s + j + 64, ..) and its absmax.
     uint32_t written = 0;
-    bool fresh = false;
+    for (int t = s + lane; t < e; t += 64) written |= 1u << static_cast<int>(slot_at(t) % kBlockSize);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) written |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(written), o, 64));
+    const bool fresh = (written & 1u) != 0;
     float seg_amax = 0.0f;
-    while (end < n_tok) {
-        const int64_t s = slot_at(end);
-        if (s < 0 || s >= capacity || s / kBlockSize != blk) break;
-        const int off = static_cast<int>(s % kBlockSize);
-        written |= 1u << off;
-        fresh |= off == 0;
-        const int64_t base = static_cast<int64_t>(end) * tok_stride + static_cast<int64_t>(h) * D;
+    for (int t = s; t < e; t++) {
+        const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
         for (int k = 0; k < kPer; k++) {
             const float a = fabsf(load_act(src, in_bf16, base + lane + 64 * k));
             seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
         }
-        end++;
     }
     seg_amax = wave_max(seg_amax);
 
@@ -64,20 +60,23 @@ __device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf1
     auto at = [&](int off, int d) -> int8_t* {
         return is_v ? block_codes + d * kBlockSize + off : block_codes + off * D + d;
     };
-    float cur_scale;
     if (fresh) {
         // Writing row 0 starts the block: earlier contents and statistics are discarded.
+        amax = seg_amax;
         cur_scale = seg_amax / 127.0f;
         if (lane == 0) {
-            absmax[sidx] = seg_amax;
+            absmax[sidx] = amax;
             scale[sidx] = cur_scale;
         }
     } else {
-        const float old_amax = absmax[sidx];
-        const float old_scale = scale[sidx];
-        cur_scale = old_scale;
-        if (seg_amax > old_amax) {
+        if (!have_stats) {
+            amax = absmax[sidx];
+            cur_scale = scale[sidx];
+        }
+        if (seg_amax > amax) {
+            const float old_scale = cur_scale;
             cur_scale = seg_amax / 127.0f;
+            amax = seg_amax;
             // Requantise every row this segment does not overwrite:
             // QuantizeSymmetric(Dequantize(q, old_scale), new_scale).
             for (int off = 0; off < kBlockSize; off++) {
@@ -90,12 +89,13 @@ __device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf1
                 }
             }
             if (lane == 0) {
-                absmax[sidx] = seg_amax;
+                absmax[sidx] = amax;
                 scale[sidx] = cur_scale;
             }
         }
     }
-    for (int t = i; t < end; t++) {
+    have_stats = true;
+    for (int t = s; t < e; t++) {
         const int off = static_cast<int>(slot_at(t) % kBlockSize);
         const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
@@ -103,6 +103,124 @@ __device__ __forceinline__ void append_int8_segment(const void* src, bool in_bf1
             const float x = load_act(src, in_bf16, base + lane + 64 * k);
             *at(off, lane + 64 * k) = quantize_symmetric(x, cur_scale);
         }
+    }
+}
+
+// Segments collected per pass of the owner's scan (a block has at most 16 rows, so more than one
+// pass only happens when slots repeat).
+constexpr int kAppendSegList = 64;
+// Threads of an int8 append workgroup: one wave per (KV head, K|V) up to 16 waves.
+constexpr int kAppendMaxThreads = 1024;
+inline int append_int8_threads(int32_t num_kv_heads) {
+    const int64_t waves = 2 * static_cast<int64_t>(num_kv_heads);
+    return static_cast<int>(64 * (waves < kAppendMaxThreads / 64 ? waves : kAppendMaxThreads / 64));
+}
+
+// Tokens per thread of the owner's coarse scan (a chunk of kAppendCoarse * blockDim.x tokens is
+// skipped when none of them lands in the block).
+constexpr int kAppendCoarse = 8;
+
+// The workgroup of token i (blockDim.x a multiple of 64, at most kAppendMaxThreads): if token i
+// is the first token of the call that lands in its block, applies every segment of that block, in
+// call order; otherwise returns. The owner reads the call's slot list once, kAppendCoarse slots per
+// thread at a time, and looks closer only at chunks that hold tokens of its block: a call of n
+// tokens costs each touched block one pass over n slots (a few memory round trips for calls of up
+// to ~16k tokens; split much larger calls).
+template <int D, typename SlotAt>
+__device__ __forceinline__ void append_int8_block(const void* k_src, const void* v_src, bool in_bf16,
+                                                  int64_t tok_stride, SlotAt slot_at, int32_t i, int32_t n_tok,
+                                                  int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                                                  float* k_absmax, float* v_absmax, int32_t num_kv_heads,
+                                                  int64_t capacity) {
+    __shared__ int s_start[kAppendSegList], s_end[kAppendSegList];
+    __shared__ int s_wcnt[2][kAppendMaxThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nthreads = blockDim.x, nwaves = nthreads >> 6;
+    auto valid = [&](int64_t sl) { return sl >= 0 && sl < capacity; };
+    // Token i's slot and its predecessor's, loaded together.
+    const int64_t slot_i = slot_at(i);
+    const int64_t slot_p = i > 0 ? slot_at(i - 1) : -1;
+    if (!valid(slot_i)) return;
+    const int64_t blk = slot_i / kBlockSize;
+    if (valid(slot_p) && slot_p / kBlockSize == blk) return;  // not the first token of its segment
+    auto in_blk = [&](int t) {
+        if (t < 0 || t >= n_tok) return false;
+        const int64_t sl = slot_at(t);
+        return valid(sl) && sl / kBlockSize == blk;
+    };
+    // Does any token of [lo, hi) land in the block? (coarse: kAppendCoarse tokens per thread)
+    auto any_in = [&](int lo, int hi) {
+        bool f = false;
+#pragma unroll
+        for (int k = 0; k < kAppendCoarse; k++) {
+            const int t = lo + k * nthreads + tid;
+            f |= t < hi && in_blk(t);
+        }
+        return __syncthreads_or(f) != 0;
+    };
+    const int coarse = kAppendCoarse * nthreads;
+    // An earlier token of the call in the block: its workgroup owns the block.
+    for (int c0 = 0; c0 < i; c0 += coarse)
+        if (any_in(c0, i)) return;
+
+    // Passes: from seg_from on, segment starts and ends are compacted, in order, into s_start /
+    // s_end until kAppendSegList segments are complete or the call ends; then they are applied.
+    int seg_from = i;
+    while (seg_from < n_tok) {
+        int nseg = 0, nstart = 0;
+        int resume = n_tok;  // where the next pass starts if this one fills the list
+        for (int c0 = seg_from; c0 < n_tok && resume == n_tok; c0 += coarse) {
+            if (!any_in(c0, n_tok)) continue;
+            const int c1 = min(n_tok, c0 + coarse);
+            for (int f0 = c0; f0 < c1; f0 += nthreads) {
+                const int t = f0 + tid;
+                const bool cur = t < c1 && in_blk(t);
+                const bool st = cur && !in_blk(t - 1);
+                const bool en = cur && !in_blk(t + 1);
+                const uint64_t ms = __ballot(st), me = __ballot(en);
+                const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+                if (lane == 0) {
+                    s_wcnt[0][wave] = __popcll(ms);
+                    s_wcnt[1][wave] = __popcll(me);
+                }
+                __syncthreads();
+                int bs = nstart, be = nseg, ts = 0, te = 0;
+                for (int w = 0; w < nwaves; w++) {
+                    if (w < wave) {
+                        bs += s_wcnt[0][w];
+                        be += s_wcnt[1][w];
+                    }
+                    ts += s_wcnt[0][w];
+                    te += s_wcnt[1][w];
+                }
+                const int rs = bs + __popcll(ms & below), re = be + __popcll(me & below);
+                if (st && rs < kAppendSegList) s_start[rs] = t;
+                if (en && re < kAppendSegList) s_end[re] = t + 1;
+                __syncthreads();
+                nstart += ts;
+                nseg += te;
+                if (nseg >= kAppendSegList) {
+                    nseg = kAppendSegList;
+                    resume = s_end[kAppendSegList - 1];
+                    break;
+                }
+            }
+        }
+        // Apply the complete segments, in order, one wave per (KV head, K|V).
+        for (int p = wave; p < 2 * num_kv_heads; p += nwaves) {
+            const int h = p >> 1;
+            const bool is_v = (p & 1) != 0;
+            float amax = 0.0f, cur_scale = 0.0f;
+            bool have = false;  // statistics of an earlier pass are re-read (written before the barrier)
+            for (int k = 0; k < nseg; k++)
+                append_int8_apply<D>(is_v ? v_src : k_src, in_bf16, tok_stride, slot_at, s_start[k], s_end[k], blk,
+                                     is_v ? v_cache : k_cache, is_v ? v_scale : k_scale, is_v ? v_absmax : k_absmax,
+                                     h, num_kv_heads, is_v, amax, cur_scale, have);
+        }
+        if (resume >= n_tok) break;
+        __syncthreads();  // this pass's statistics and codes are visible to the next pass's waves
+        seg_from = resume;
     }
 }
 

@@ -141,18 +141,20 @@ __global__ __launch_bounds__(kCopyThreads) void write_block_plain_kernel(CacheRe
     }
 }
 
-// int8 caches: the quantising append of pa_kv_append (one segment: the block's tokens), one wave
-// per (head, K|V).
+// int8 caches: the quantising append of pa_kv_append (one segment: the block's tokens, row 0
+// included, so the block starts afresh), one wave per (head, K|V).
 template <int D>
 __global__ __launch_bounds__(64) void write_block_int8_kernel(CacheRefs c, int32_t block, int32_t tokens,
                                                              const float* __restrict__ k_in,
                                                              const float* __restrict__ v_in) {
     const bool is_v = blockIdx.y != 0;
-    const int64_t capacity = static_cast<int64_t>(c.num_blocks) * pa::kBlockSize;
-    pa::append_int8_segment<D>(is_v ? static_cast<const void*>(v_in) : static_cast<const void*>(k_in), false,
-                               static_cast<int64_t>(c.hkv) * D, [&](int t) { return static_cast<int64_t>(block) * pa::kBlockSize + t; }, 0, tokens,
-                               reinterpret_cast<int8_t*>(is_v ? c.v : c.k), c.stat[is_v ? 1 : 0],
-                               c.stat[is_v ? 3 : 2], static_cast<int>(blockIdx.x), c.hkv, capacity, is_v);
+    float amax = 0.0f, scale = 0.0f;
+    bool have = false;
+    pa::append_int8_apply<D>(is_v ? static_cast<const void*>(v_in) : static_cast<const void*>(k_in), false,
+                             static_cast<int64_t>(c.hkv) * D,
+                             [&](int t) { return static_cast<int64_t>(block) * pa::kBlockSize + t; }, 0, tokens, block,
+                             reinterpret_cast<int8_t*>(is_v ? c.v : c.k), c.stat[is_v ? 1 : 0], c.stat[is_v ? 3 : 2],
+                             static_cast<int>(blockIdx.x), c.hkv, is_v, amax, scale, have);
 }
 
 // Checks shared by the entry points; fills `c`. need_absmax: int8 needs the running absmax too

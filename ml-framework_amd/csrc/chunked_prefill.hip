@@ -489,6 +489,8 @@ extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg,
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: null pointer");
     if (cfg->kv_dtype == PA_DTYPE_FP32)
         return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: the cache must be BF16 or INT8");
+    if (cfg->head_dim < 64)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: head_dim must be 64, 128 or 256");
     if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: int8 cache needs k_scale and v_scale");
     const uint32_t masks = cfg->flags & (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK);

@@ -54,6 +54,9 @@ struct DecodeArgs {
     // h (a range has slots for its first and last row portions only, and grouped rows never write
     // the output directly).
     int32_t row_slot_base;
+    // MFMA kernel: units (range, KV head) the workspace has slots for (2 per unit), computed on the
+    // host from the call's shape; the merges follow no slot index at or past 2 * max_units.
+    int64_t max_units;
 };
 
 // Shared-prefix plan, in device memory: num_groups records {first sequence, members, shared
@@ -138,8 +141,8 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 // value its lane computed. An empty range leaves M = -inf, L = 0, o = 0.
 template <int D, typename PidxOf>
 __device__ __forceinline__ void merge_range(const DecodeArgs& a, int g, int pbeg, int pend, PidxOf pidx_of, float& M,
-                                            float& L, float (&o)[D / 64]) {
-    constexpr int DPL = D / 64;  // dims per lane
+                                            float& L, float (&o)[(D + 63) / 64]) {
+    constexpr int DPL = (D + 63) / 64;  // dims per lane (lanes past D hold none when D = 32)
     constexpr int UNROLL = 16;   // partials whose output loads are issued together
     const int lane = threadIdx.x & 63;
     M = -INFINITY;
@@ -161,7 +164,7 @@ __device__ __forceinline__ void merge_range(const DecodeArgs& a, int g, int pbeg
                 if (u + j < cnt) {
                     const int64_t pj = pidx_of(p0 + u + j, g);
 #pragma unroll
-                    for (int k = 0; k < DPL; k++) x[j][k] = a.ws_o[pj * D + lane + 64 * k];
+                    for (int k = 0; k < DPL; k++) x[j][k] = lane + 64 * k < D ? a.ws_o[pj * D + lane + 64 * k] : 0.0f;
                 } else {
 #pragma unroll
                     for (int k = 0; k < DPL; k++) x[j][k] = 0.0f;
@@ -192,7 +195,7 @@ __device__ __forceinline__ void merge_range(const DecodeArgs& a, int g, int pbeg
 // group. pidx_of(u, g) is the workspace row of partial u of head g of the group.
 template <int D, typename PidxOf>
 __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, int kvh, int nparts, PidxOf pidx_of) {
-    constexpr int DPL = D / 64;
+    constexpr int DPL = (D + 63) / 64;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = a.group;
@@ -202,7 +205,8 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
         merge_range<D>(a, g, 0, nparts, pidx_of, M, L, o);
         const float inv = 1.0f / L;
 #pragma unroll
-        for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = o[k] * inv;
+        for (int k = 0; k < DPL; k++)
+            if (lane + 64 * k < D) a.out[row * D + lane + 64 * k] = o[k] * inv;
     }
 }
 
@@ -211,8 +215,8 @@ __device__ __forceinline__ void merge_partitions(const DecodeArgs& a, int seq, i
 template <int D, typename PidxOf>
 __device__ __forceinline__ void merge_head_wide(const DecodeArgs& a, int seq, int kvh, int g, int nparts,
                                                 PidxOf pidx_of) {
-    constexpr int DPL = D / 64;
-    __shared__ float s_m[4], s_l[4], s_o[4][D];
+    constexpr int DPL = (D + 63) / 64;
+    __shared__ float s_m[4], s_l[4], s_o[4][DPL * 64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = (nparts + 3) / 4;
@@ -240,7 +244,8 @@ __device__ __forceinline__ void merge_head_wide(const DecodeArgs& a, int seq, in
     const int64_t row = static_cast<int64_t>(seq) * a.num_kv_heads * a.group + kvh * a.group + g;
     const float inv = 1.0f / lt;
 #pragma unroll
-    for (int k = 0; k < DPL; k++) a.out[row * D + lane + 64 * k] = ot[k] * inv;
+    for (int k = 0; k < DPL; k++)
+        if (lane + 64 * k < D) a.out[row * D + lane + 64 * k] = ot[k] * inv;
 }
 
 // Merge pass: one workgroup per (KV head, sequence).
@@ -286,6 +291,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
     const int64_t C = split_range_blocks(a, total);
     const int64_t w1 = R0 / C, w2 = (R0 + nbr - 1) / C;
     if (w1 == w2) return;  // written whole by the decode kernel
+    if ((w2 + 1) * Hkv > a.max_units) return;  // slots the workspace does not have
     const bool starts_inside = R0 != w1 * C;
     const int G = a.group;
     merge_partitions<D>(a, seq, kvh, static_cast<int>(w2 - w1 + 1), [&](int u, int g) {
@@ -346,6 +352,10 @@ __global__ __launch_bounds__(256) void paged_decode_merge_prefix_kernel(const De
     }
     if (grp < 0 && ns <= 1) return;  // written whole by the decode kernel
     if (ns + np == 0) return;
+    // Unit slots the workspace does not have (a prefix table that does not fit the call). Row slots
+    // are bounded by the host-checked group count.
+    if (ns > 1 && (w1 + ns) * Hkv > a.max_units) return;
+    if (np > 1 && (pw1 + np) * Hkv > a.max_units) return;
     // A row inside one range left its partial in its row slot, a split row one per range.
     merge_head_wide<D>(a, seq, kvh, static_cast<int>(blockIdx.z), ns + np, [&](int u, int g) -> int64_t {
         if (u < ns) {
@@ -453,12 +463,13 @@ int device_cus();
 // in all; records the worker count in a.split_grid (the merge kernel needs it).
 // shared: the shared-prefix decode (a.plan, a.num_groups; no append), whose row list is the
 // num_groups prefix rows and then one suffix row per sequence.
-void launch_decode_mfma_d64(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
-                            int64_t max_grid, hipStream_t s);
-void launch_decode_mfma_d128(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
-                             int64_t max_grid, hipStream_t s);
-void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
-                             int64_t max_grid, hipStream_t s);
+template <int D>
+void launch_decode_mfma(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
+                        int64_t max_grid, hipStream_t s);
+extern template void launch_decode_mfma<32>(DecodeArgs&, int, bool, bool, bool, int, int64_t, hipStream_t);
+extern template void launch_decode_mfma<64>(DecodeArgs&, int, bool, bool, bool, int, int64_t, hipStream_t);
+extern template void launch_decode_mfma<128>(DecodeArgs&, int, bool, bool, bool, int, int64_t, hipStream_t);
+extern template void launch_decode_mfma<256>(DecodeArgs&, int, bool, bool, bool, int, int64_t, hipStream_t);
 // fp32 caches: grid (max_parts, Hkv, num_seqs); returns false for an uncompiled shape.
 bool launch_decode_fp32(const DecodeArgs& a, int head_dim, dim3 grid, hipStream_t s);
 

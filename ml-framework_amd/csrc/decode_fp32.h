@@ -17,7 +17,7 @@ __global__ __launch_bounds__(256) void paged_decode_fp32_kernel(const DecodeArgs
     constexpr int NBW = PART / 64; // blocks per wave
     constexpr int TPT = PART / 256;
     constexpr int TILE = 16 * D;
-    static_assert(CH >= 16 && CH <= 64, "fp32 kernel covers head_dim 64..256");
+    static_assert(CH >= 8 && CH <= 64, "fp32 kernel covers head_dim 32..256");
 
     __shared__ float s_logits[G][PART];
     __shared__ float s_red[4][G];

@@ -25,6 +25,7 @@ bool launch_d(const DecodeArgs& a, dim3 grid, hipStream_t s) {
 
 bool launch_decode_fp32(const DecodeArgs& a, int head_dim, dim3 grid, hipStream_t s) {
     switch (head_dim) {
+        case 32: return launch_d<32>(a, grid, s);
         case 64: return launch_d<64>(a, grid, s);
         case 128: return launch_d<128>(a, grid, s);
         case 256: return launch_d<256>(a, grid, s);

@@ -99,7 +99,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
     constexpr int NT = D / 16;     // PV n-tiles of 16 dims
     constexpr int TILE = 16 * D;   // elements per (block, KV head) tile
-    constexpr int NPL = D / 64;    // appended-token values per lane
+    constexpr int NPL = D >= 64 ? D / 64 : 1;  // appended-token values per lane (lanes < D when D = 32)
 
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4;  // token group (QK C rows) / k group of the MFMA operands
@@ -233,7 +233,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             my_vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + kvh];
         }
         if constexpr (APPEND) {
-            if (j_app >= 0) {
+            if (j_app >= 0 && lane * NPL < D) {
                 const int64_t src = (static_cast<int64_t>(seq) * Hkv + kvh) * D + lane * NPL;
 #pragma unroll
                 for (int w = 0; w < NW; w++) {
@@ -311,10 +311,12 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                     vw[w] = nv_raw[w];
                     asm volatile("" : "+v"(kw[w]), "+v"(vw[w]));
                 }
+                if (lane * NPL < D) {
 #pragma unroll
-                for (int e = 0; e < NPL; e++) {
-                    s_new[lane * NPL + e] = new_val(kw, e);
-                    s_new[D + lane * NPL + e] = new_val(vw, e);
+                    for (int e = 0; e < NPL; e++) {
+                        s_new[lane * NPL + e] = new_val(kw, e);
+                        s_new[D + lane * NPL + e] = new_val(vw, e);
+                    }
                 }
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the stores have landed in LDS
                 __builtin_amdgcn_wave_barrier();

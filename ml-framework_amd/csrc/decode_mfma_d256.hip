@@ -1,50 +1,4 @@
-// decode_mfma_d256.hip -- instantiations of the MFMA paged-decode kernel for head_dim 256.
-#include "decode_mfma.h"
+// decode_mfma_d256.hip -- the head_dim 256 instances of the MFMA paged-decode kernel.
+#include "decode_mfma_launch.h"
 
-namespace pa {
-namespace {
-
-template <int D, int KV, bool QF32, bool APPEND, bool SHARED>
-void launch_one(DecodeArgs& a, int num_seqs, int64_t max_grid, hipStream_t s) {
-    auto kern = paged_decode_mfma_persistent_kernel<D, KV, QF32, APPEND, SHARED>;
-    // Resident workgroups per CU for this instance (queried once; read-only afterwards).
-    constexpr int waves = decode_waves(D);
-    static const int per_cu = [&] {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 64 * waves, 0) != hipSuccess || n < 1) n = 1;
-        return n;
-    }();
-    int64_t workers = static_cast<int64_t>(device_cus()) * per_cu * waves;
-    if (workers > kMaxDecodeWorkers) workers = kMaxDecodeWorkers;
-    if (workers >= a.num_kv_heads) workers -= workers % a.num_kv_heads;  // whole ranges (one unit per KV head)
-    if (workers > max_grid) workers = max_grid;
-    if (workers < 1) workers = 1;
-    a.split_grid = static_cast<int32_t>(workers);
-    const int64_t nwg = (workers + waves - 1) / waves;
-    kern<<<static_cast<unsigned>(nwg), 64 * waves, 0, s>>>(a, num_seqs);
-}
-
-template <int KV, bool QF32>
-void pick(DecodeArgs& a, bool append, bool shared, int num_seqs, int64_t max_grid, hipStream_t s) {
-    if (shared) launch_one<256, KV, QF32, false, true>(a, num_seqs, max_grid, s);
-    else if (append) launch_one<256, KV, QF32, true, false>(a, num_seqs, max_grid, s);
-    else launch_one<256, KV, QF32, false, false>(a, num_seqs, max_grid, s);
-}
-
-}  // namespace
-
-void launch_decode_mfma_d256(DecodeArgs& a, int kv_dtype, bool q_f32, bool append, bool shared, int num_seqs,
-                            int64_t max_grid, hipStream_t s) {
-    if (kv_dtype == PA_DTYPE_BF16) {
-        if (q_f32) pick<PA_DTYPE_BF16, true>(a, append, shared, num_seqs, max_grid, s);
-        else pick<PA_DTYPE_BF16, false>(a, append, shared, num_seqs, max_grid, s);
-    } else if (shared) {
-        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false, true>(a, num_seqs, max_grid, s);
-        else launch_one<256, PA_DTYPE_INT8, false, false, true>(a, num_seqs, max_grid, s);
-    } else {  // int8 caches are appended by a separate launch before the decode
-        if (q_f32) launch_one<256, PA_DTYPE_INT8, true, false, false>(a, num_seqs, max_grid, s);
-        else launch_one<256, PA_DTYPE_INT8, false, false, false>(a, num_seqs, max_grid, s);
-    }
-}
-
-}  // namespace pa
+template void pa::launch_decode_mfma<256>(pa::DecodeArgs&, int, bool, bool, bool, int, int64_t, hipStream_t);

@@ -101,19 +101,18 @@ __global__ __launch_bounds__(256) void append_plain_kernel(
     }
 }
 
-// int8 caches: one wave per (token, KV head, K|V); the segment logic is append_int8_segment.
+// int8 caches: one workgroup per token of the call; the workgroup of the first token that lands in
+// a block applies all of that block's segments (append_int8_block), one wave per (KV head, K|V).
 template <int D>
-__global__ __launch_bounds__(64) void append_int8_kernel(
+__global__ __launch_bounds__(pa::kAppendMaxThreads) void append_int8_kernel(
     const void* __restrict__ k_new, const void* __restrict__ v_new, bool in_bf16,
     const int64_t* __restrict__ slot_mapping, int32_t n_tok, int8_t* __restrict__ k_cache,
     int8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
     float* __restrict__ k_absmax, float* __restrict__ v_absmax, int32_t num_kv_heads, int64_t capacity,
     int64_t tok_stride) {
-    const bool is_v = blockIdx.z != 0;
-    pa::append_int8_segment<D>(is_v ? v_new : k_new, in_bf16, tok_stride, [&](int t) { return slot_mapping[t]; },
-                               static_cast<int32_t>(blockIdx.x), n_tok, is_v ? v_cache : k_cache,
-                               is_v ? v_scale : k_scale, is_v ? v_absmax : k_absmax,
-                               static_cast<int>(blockIdx.y), num_kv_heads, capacity, is_v);
+    pa::append_int8_block<D>(k_new, v_new, in_bf16, tok_stride, [&](int t) { return slot_mapping[t]; },
+                             static_cast<int32_t>(blockIdx.x), n_tok, k_cache, v_cache, k_scale, v_scale, k_absmax,
+                             v_absmax, num_kv_heads, capacity);
 }
 
 }  // namespace
@@ -164,25 +163,24 @@ pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, c
     } else {
         if (!k_scale || !v_scale || !k_absmax || !v_absmax)
             return set_error(PA_ERROR_INVALID_ARGUMENT, fn + ": int8 cache needs scales and absmax");
-        if (cfg->num_kv_heads > 65535) return set_error(PA_ERROR_INVALID_CONFIG, fn + ": too many KV heads");
-        dim3 grid(n_tok, cfg->num_kv_heads, 2);
+        const int threads = append_int8_threads(cfg->num_kv_heads);
         auto* kc = static_cast<int8_t*>(k_cache);
         auto* vc = static_cast<int8_t*>(v_cache);
         switch (cfg->head_dim) {
             case 64:
-                append_int8_kernel<64><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc, k_scale,
-                                                           v_scale, k_absmax, v_absmax, cfg->num_kv_heads, capacity,
-                                                           tok_stride);
+                append_int8_kernel<64><<<n_tok, threads, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                                 k_scale, v_scale, k_absmax, v_absmax,
+                                                                 cfg->num_kv_heads, capacity, tok_stride);
                 break;
             case 128:
-                append_int8_kernel<128><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
-                                                            k_scale, v_scale, k_absmax, v_absmax, cfg->num_kv_heads,
-                                                            capacity, tok_stride);
+                append_int8_kernel<128><<<n_tok, threads, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                                  k_scale, v_scale, k_absmax, v_absmax,
+                                                                  cfg->num_kv_heads, capacity, tok_stride);
                 break;
             default:
-                append_int8_kernel<256><<<grid, 64, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
-                                                            k_scale, v_scale, k_absmax, v_absmax, cfg->num_kv_heads,
-                                                            capacity, tok_stride);
+                append_int8_kernel<256><<<n_tok, threads, 0, s>>>(k_new, v_new, in_bf16, slot_mapping, n_tok, kc, vc,
+                                                                  k_scale, v_scale, k_absmax, v_absmax,
+                                                                  cfg->num_kv_heads, capacity, tok_stride);
                 break;
         }
     }

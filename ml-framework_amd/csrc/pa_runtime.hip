@@ -52,10 +52,13 @@ pa_status check_config(const pa_config* cfg, const char* fn) {
     if (cfg->num_q_heads <= 0 || cfg->num_kv_heads <= 0 || cfg->num_q_heads % cfg->num_kv_heads != 0)
         return set_error(PA_ERROR_INVALID_CONFIG,
                          f + ": num_q_heads must be a positive multiple of num_kv_heads");
-    if (cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256)
-        return set_error(PA_ERROR_UNSUPPORTED, f + ": head_dim must be 64, 128 or 256");
+    if (cfg->head_dim != 32 && cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256)
+        return set_error(PA_ERROR_UNSUPPORTED, f + ": head_dim must be 32, 64, 128 or 256");
     if (cfg->kv_dtype != PA_DTYPE_FP32 && cfg->kv_dtype != PA_DTYPE_BF16 && cfg->kv_dtype != PA_DTYPE_INT8)
         return set_error(PA_ERROR_UNSUPPORTED, f + ": kv_dtype must be FP32, BF16 or INT8");
+    // int8 codes meet the int8 MFMA (64 dims per instruction) and 64-lane quantiser rows.
+    if (cfg->kv_dtype == PA_DTYPE_INT8 && cfg->head_dim < 64)
+        return set_error(PA_ERROR_UNSUPPORTED, f + ": int8 caches take head_dim 64, 128 or 256");
     if (cfg->q_dtype != PA_DTYPE_FP32 && cfg->q_dtype != PA_DTYPE_BF16)
         return set_error(PA_ERROR_UNSUPPORTED, f + ": q_dtype must be FP32 or BF16");
     if (cfg->num_blocks < 0) return set_error(PA_ERROR_INVALID_CONFIG, f + ": num_blocks < 0");

@@ -122,13 +122,13 @@ __global__ __launch_bounds__(256) void append_last_token_fp32_kernel(const Decod
 
 // int8 caches, pa_paged_decode_append: the new token of every sequence (position T - 1, T the
 // clamped context length) is appended by the quantising append of pa_kv_append, as token i = seq
-// i of one call, before the decode reads the cache. One wave per (sequence, KV head, K|V). (Done
-// inside the decode kernel instead, the requantisation stalls the wave that owns each row's last
-// block mid-stream; a separate launch costs less.)
+// i of one call, before the decode reads the cache: one workgroup per sequence, the owner of each
+// block applying its tokens, one wave per (KV head, K|V). (Done inside the decode kernel instead,
+// the requantisation stalls the wave that owns each row's last block mid-stream; a separate launch
+// costs less.)
 template <int D>
-__global__ __launch_bounds__(64) void append_last_token_int8_kernel(const DecodeArgs a, int32_t num_seqs) {
-    const bool is_v = blockIdx.z != 0;
-    const int i = static_cast<int>(blockIdx.x), lane = static_cast<int>(threadIdx.x);
+__global__ __launch_bounds__(pa::kAppendMaxThreads) void append_last_token_int8_kernel(const DecodeArgs a,
+                                                                                      int32_t num_seqs) {
     const int64_t capacity = static_cast<int64_t>(a.num_blocks) * pa::kBlockSize;
     auto last_slot = [&](int t) -> int64_t {
         const int T = clamp_len(a, a.context_lens[t]);
@@ -136,23 +136,11 @@ __global__ __launch_bounds__(64) void append_last_token_int8_kernel(const Decode
         const int32_t bid = a.block_tables[static_cast<int64_t>(t) * a.max_blocks_per_seq + (T - 1) / pa::kBlockSize];
         return bid >= 0 ? static_cast<int64_t>(bid) * pa::kBlockSize + (T - 1) % pa::kBlockSize : -1;
     };
-    // The slots of tokens i - 1 .. i + 62, one per lane, looked up together (a segment rarely spans
-    // more than one token here, and each lookup is two dependent loads).
-    const int t_l = i - 1 + lane;
-    const int64_t my_slot = t_l >= 0 && t_l < num_seqs ? last_slot(t_l) : -1;
-    auto slot_at = [&](int t) -> int64_t {
-        const int k = t - i + 1;
-        if (k < 0 || k >= 64) return last_slot(t);
-        const uint64_t u = static_cast<uint64_t>(my_slot);
-        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), k);
-        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), k);
-        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-    };
-    pa::append_int8_segment<D>(is_v ? a.v_new : a.k_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D,
-                               slot_at, i,
-                               num_seqs, static_cast<int8_t*>(const_cast<void*>(is_v ? a.v_cache : a.k_cache)),
-                               const_cast<float*>(is_v ? a.v_scale : a.k_scale), is_v ? a.v_absmax : a.k_absmax,
-                               static_cast<int>(blockIdx.y), a.num_kv_heads, capacity, is_v);
+    pa::append_int8_block<D>(a.k_new, a.v_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D, last_slot,
+                             static_cast<int32_t>(blockIdx.x), num_seqs,
+                             static_cast<int8_t*>(const_cast<void*>(a.k_cache)),
+                             static_cast<int8_t*>(const_cast<void*>(a.v_cache)), const_cast<float*>(a.k_scale),
+                             const_cast<float*>(a.v_scale), a.k_absmax, a.v_absmax, a.num_kv_heads, capacity);
 }
 
 }  // namespace
@@ -239,6 +227,7 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
     a.scale = pa::resolve_scale(cfg);
     const int64_t max_units = fp32 ? 0 : mfma_max_units(cfg, num_seqs, max_len, part);
+    a.max_units = max_units;
     if (need > 0) {
         const int64_t rows = fp32 ? static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts : 2 * max_units * G;
         a.ws_o = static_cast<float*>(workspace);
@@ -257,6 +246,7 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
         if (max_parts > 1) {
             dim3 mgrid(cfg->num_kv_heads, num_seqs);
             switch (cfg->head_dim) {
+                case 32: pa::paged_decode_merge_kernel<32><<<mgrid, 256, 0, s>>>(a); break;
                 case 64: pa::paged_decode_merge_kernel<64><<<mgrid, 256, 0, s>>>(a); break;
                 case 128: pa::paged_decode_merge_kernel<128><<<mgrid, 256, 0, s>>>(a); break;
                 default: pa::paged_decode_merge_kernel<256><<<mgrid, 256, 0, s>>>(a); break;
@@ -268,24 +258,26 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     const int64_t max_grid = max_units > 0 ? max_units : 1;
     if (append && cfg->kv_dtype == PA_DTYPE_INT8 && num_seqs > 0) {
-        dim3 agrid(num_seqs, cfg->num_kv_heads, 2);
+        const int threads = pa::append_int8_threads(cfg->num_kv_heads);
         switch (cfg->head_dim) {
-            case 64: append_last_token_int8_kernel<64><<<agrid, 64, 0, s>>>(a, num_seqs); break;
-            case 128: append_last_token_int8_kernel<128><<<agrid, 64, 0, s>>>(a, num_seqs); break;
-            default: append_last_token_int8_kernel<256><<<agrid, 64, 0, s>>>(a, num_seqs); break;
+            case 64: append_last_token_int8_kernel<64><<<num_seqs, threads, 0, s>>>(a, num_seqs); break;
+            case 128: append_last_token_int8_kernel<128><<<num_seqs, threads, 0, s>>>(a, num_seqs); break;
+            default: append_last_token_int8_kernel<256><<<num_seqs, threads, 0, s>>>(a, num_seqs); break;
         }
         PA_HIP_CHECK(hipGetLastError());
         append = false;  // the decode below reads the appended cache
     }
     switch (cfg->head_dim) {
-        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
-        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
-        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        case 32: pa::launch_decode_mfma<32>(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        case 64: pa::launch_decode_mfma<64>(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        case 128: pa::launch_decode_mfma<128>(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
+        default: pa::launch_decode_mfma<256>(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
     if (max_units > cfg->num_kv_heads) {  // more than one range: a row may span two
         dim3 mgrid(cfg->num_kv_heads, num_seqs);
         switch (cfg->head_dim) {
+            case 32: pa::paged_decode_merge_split_kernel<32><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
             case 64: pa::paged_decode_merge_split_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
             case 128: pa::paged_decode_merge_split_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
             default: pa::paged_decode_merge_split_kernel<256><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
@@ -295,16 +287,18 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     return pa::clear_error();
 }
 
-// Calls with more sequences than the persistent kernel's prefix table are issued in chunks of
-// sequences (each chunk is an independent ragged batch on the same stream and workspace).
+// Calls with more sequences than one launch takes (the persistent kernel's prefix table for bf16 /
+// int8 caches, the grid's z extent for fp32 caches) are issued in chunks of sequences (each chunk
+// is an independent ragged batch on the same stream and workspace).
 pa_status decode_impl(const char* fn, bool append, pa_stream* stream, const pa_config* cfg, float* out,
                       const void* q, const void* k_new, const void* v_new, const void* k_cache,
                       const void* v_cache, const float* k_scale, const float* v_scale, float* k_absmax,
                       float* v_absmax, const int32_t* block_tables, const int32_t* context_lens,
                       int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len, void* workspace,
                       size_t workspace_bytes) {
-    constexpr int32_t kChunk = pa::kMaxPersistentSeqs - 1;
-    if (!cfg || num_seqs <= kChunk || cfg->kv_dtype == PA_DTYPE_FP32)
+    // MFMA kernels: the persistent kernel's per-sequence tables; fp32: the grid's z extent.
+    const int32_t kChunk = cfg && cfg->kv_dtype == PA_DTYPE_FP32 ? 65535 : pa::kMaxPersistentSeqs - 1;
+    if (!cfg || num_seqs <= kChunk)
         return decode_chunk(fn, append, stream, cfg, out, q, k_new, v_new, k_cache, v_cache, k_scale, v_scale,
                             k_absmax, v_absmax, block_tables, context_lens, num_seqs, max_blocks_per_seq,
                             max_context_len, workspace, workspace_bytes);
@@ -531,6 +525,7 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
     a.plan = static_cast<const int32_t*>(plan);
     a.num_groups = num_groups;
     const int64_t max_units = mfma_max_units(cfg, num_seqs, max_len, 0);
+    a.max_units = max_units;
     const int64_t rows = prefix_slots(cfg, num_seqs, max_len) * pa::kPrefixSlotRows;
     a.row_slot_base = static_cast<int32_t>(2 * max_units);
     a.ws_o = static_cast<float*>(workspace);
@@ -541,13 +536,15 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     const int64_t max_grid = max_units > 0 ? max_units : 1;
     switch (cfg->head_dim) {
-        case 64: pa::launch_decode_mfma_d64(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
-        case 128: pa::launch_decode_mfma_d128(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
-        default: pa::launch_decode_mfma_d256(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        case 32: pa::launch_decode_mfma<32>(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        case 64: pa::launch_decode_mfma<64>(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        case 128: pa::launch_decode_mfma<128>(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
+        default: pa::launch_decode_mfma<256>(a, cfg->kv_dtype, qf32, false, true, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
     dim3 mgrid(cfg->num_kv_heads, num_seqs, G);
     switch (cfg->head_dim) {
+        case 32: pa::paged_decode_merge_prefix_kernel<32><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
         case 64: pa::paged_decode_merge_prefix_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
         case 128: pa::paged_decode_merge_prefix_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
         default: pa::paged_decode_merge_prefix_kernel<256><<<mgrid, 256, 0, s>>>(a, num_seqs); break;

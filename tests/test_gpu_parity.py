@@ -1,8 +1,8 @@
 """GPU parity of libpa_hip.so against the CPU oracle, called through the C-ABI.
 
 Bar: slot mapping, fp32/bf16 stores and int8 codes/scales/absmax are bit-exact; attention
-outputs satisfy |gpu - oracle| <= atol + rtol*|oracle| with (2e-3, 1e-2) for fp32/bf16 KV and
-(2e-2, 1e-2) for int8 KV (tests/helpers.py), accumulation in fp32.
+outputs satisfy |gpu - oracle| <= atol + rtol*|oracle| with (2e-3, 1e-2) for bf16 KV, (2e-2, 1e-2)
+for int8 KV and (1e-5, 1e-4) for fp32 KV (tests/helpers.py), accumulation in fp32.
 """
 import os
 
@@ -191,11 +191,51 @@ def test_append_int8_bit_exact(stream, D, q_dtype):
     step(slots, k, v)
 
 
+@pytest.mark.parametrize("D,q_dtype", [(128, 0), (64, 1), (256, 0)])
+def test_append_int8_out_of_order_bit_exact(stream, D, q_dtype):
+    """A block's tokens split by -1 padding, revisited after other blocks' tokens, a slot written
+    twice, out-of-range slots, and a random scatter with ~80 segments per block (more than one pass
+    of the owner's segment list): the first token of the call in a block owns it and applies its
+    segments in call order, so the GPU matches the oracle's sequential append bit for bit."""
+    rng = np.random.default_rng(90 + D)
+    nb, hkv = 12, 4
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=2, q_dtype=q_dtype,
+                         num_blocks=nb)
+    host = dict(kc=np.zeros((nb, hkv, 16, D), np.int8), vc=np.zeros((nb, hkv, 16, D), np.int8),
+                ks=np.zeros((nb, hkv), np.float32), vs=np.zeros((nb, hkv), np.float32),
+                ka=np.zeros((nb, hkv), np.float32), va=np.zeros((nb, hkv), np.float32))
+    dev = {n: to_gpu(a) for n, a in host.items()}
+
+    def step(slots, scale_choices):
+        slots = np.asarray(slots, np.int64)
+        mult = rng.choice(scale_choices, size=(len(slots), 1, 1)).astype(np.float32)
+        k = (rng.standard_normal((len(slots), hkv, D), dtype=np.float32) * mult).astype(np.float32)
+        v = (rng.standard_normal((len(slots), hkv, D), dtype=np.float32) * mult[::-1]).astype(np.float32)
+        if q_dtype == 1:
+            k, v = orc.bf16_from_f32(k), orc.bf16_from_f32(v)
+        orc.kv_append(cfg, k, v, slots, host["kc"], host["vc"], host["ks"], host["vs"], host["ka"], host["va"])
+        pa.kv_append(stream, cfg, to_gpu(k), to_gpu(v), to_gpu(slots), len(slots), dev["kc"], dev["vc"],
+                     dev["ks"], dev["vs"], dev["ka"], dev["va"])
+        _sync()
+        for n, a in host.items():
+            np.testing.assert_array_equal(to_np(dev[n]), a, err_msg=n)
+
+    step(np.arange(nb * 16), [1.0])  # every block filled in order
+    # block 1 split by padding and revisited, block 3 and 5 in between, slot 22 twice, 97 / 500 invalid
+    step([19, 20, -1, 21, 48, 49, 22, 22, 87, -1, -1, 50, 25, nb * 16 + 1, 26, 500, 16 + 15, 16 + 0], [0.5, 4.0])
+    # a random scatter over 5 blocks: ~80 segments per block, many with scale growth
+    slots = rng.choice(np.arange(16 * 5, 16 * 10), size=400).astype(np.int64)
+    slots[rng.random(400) < 0.1] = -1
+    step(slots, [0.25, 1.0, 8.0])
+
+
 # ---- decode -----------------------------------------------------------------------------------------
 def test_decode_c1_fp32(stream):
+    """C1, the CPU-parity configuration (fp32 cache and query, VALU kernel), at the fp32 bar."""
     w = wl.make_c1()
     got, ref = run_decode(w, 101, stream)
-    check_close(got, ref, **tol_for(0), what="C1")
+    err = check_close(got, ref, **tol_for(0), what="C1")
+    assert err < 1e-5
 
 
 def test_decode_c2_bf16_full(stream):

@@ -228,10 +228,11 @@ def test_prefix_decode_graph_replay_matches_eager():
         dev.close()
 
 
-def test_c5_full_size_split_and_prefix_agree(stream):
-    """Full C5 (8 sequences of 16-32k tokens, 512 shared blocks): the default split, a 64-token
-    split (about 500 partials per row: the merge's multi-round path) and the shared-prefix decode
-    compute the same attention in different orders and agree within the bf16 tolerance."""
+def test_c5_full_size_vs_oracle(stream):
+    """Full C5 (8 sequences of 16-32k tokens, 512 shared blocks): pa_paged_decode with the default
+    split and pa_paged_decode_prefix, the two calls bench.py times, each against the oracle's
+    whole-context decode; a 64-token split (about 500 partials per row: the merge's multi-round
+    path) against the default split."""
     import torch
 
     w = wl.make_c5()
@@ -270,5 +271,8 @@ def test_c5_full_size_split_and_prefix_agree(stream):
                            ws, wsb)
     _sync()
     outs["prefix"] = to_np(out).copy()
+    ref = orc.paged_decode(cfg, to_np(q, np.uint16), to_np(kc, np.uint16), to_np(vc, np.uint16), None, None,
+                           w.block_tables, w.context_lens, n_threads=NTHREADS)
+    check_close(outs["default"], ref, **tol_for(1), what="C5 pa_paged_decode vs oracle")
+    check_close(outs["prefix"], ref, **tol_for(1), what="C5 pa_paged_decode_prefix vs oracle")
     check_close(outs["p64"], outs["default"], **tol_for(1), what="C5 64-token split vs default")
-    check_close(outs["prefix"], outs["default"], **tol_for(1), what="C5 shared-prefix vs default")

@@ -356,6 +356,52 @@ def test_append_int8_policy_invariants():
     assert ka[2, 0] == np.abs(z[0, 0]).max()
 
 
+def _segments(slots, nb):
+    """Maximal runs of consecutive valid slots that lie in one block: (start, end) pairs."""
+    segs, i, n = [], 0, len(slots)
+    while i < n:
+        if not 0 <= slots[i] < nb * 16:
+            i += 1
+            continue
+        j = i + 1
+        while j < n and 0 <= slots[j] < nb * 16 and slots[j] // 16 == slots[i] // 16:
+            j += 1
+        segs.append((i, j))
+        i = j
+    return segs
+
+
+def test_append_int8_call_equals_its_segments_in_order():
+    """The int8 append of a call whose blocks arrive out of order (runs split by -1 padding, a
+    block revisited after other blocks, a slot written twice) equals its segments appended one by
+    one as separate calls, in call order: the rule the GPU's per-block owner follows."""
+    rng = np.random.default_rng(21)
+    nb, H, D = 6, 2, 64
+    cfg = pa.make_config(num_q_heads=H, num_kv_heads=H, head_dim=D, kv_dtype=2, num_blocks=nb)
+    base = [np.zeros((nb, H, 16, D), np.int8) for _ in range(2)] + [np.zeros((nb, H), f32) for _ in range(4)]
+    fill = rng.standard_normal((nb * 16, H, D)).astype(f32)
+    orc.kv_append(cfg, fill, fill, np.arange(nb * 16, dtype=np.int64), *base)
+    slots = np.array([16 + 3, 16 + 4, -1, 16 + 5, 48, 49, 16 + 6, 16 + 6, 80 + 7, -1, -1, 48 + 2, 16 + 9,
+                      nb * 16 + 1, 16 + 10], np.int64)
+    x = (rng.standard_normal((len(slots), H, D)) * rng.choice([0.5, 4.0], size=(len(slots), 1, 1))).astype(f32)
+    whole = [a.copy() for a in base]
+    orc.kv_append(cfg, x, x, slots, *whole)
+    piecewise = [a.copy() for a in base]
+    segs = _segments(slots, nb)
+    assert len(segs) == 8 and sum(slots[a] // 16 == 1 for a, _ in segs) == 5  # block 1 comes back 5 times
+    for s0, s1 in segs:
+        xs = np.ascontiguousarray(x[s0:s1])
+        orc.kv_append(cfg, xs, xs, np.ascontiguousarray(slots[s0:s1]), *piecewise)
+    for a, b in zip(whole, piecewise):
+        np.testing.assert_array_equal(a, b)
+    # within one segment the later of two tokens with the same slot wins
+    one = [a.copy() for a in base]
+    xs = np.ascontiguousarray(x[6:8])
+    orc.kv_append(cfg, xs, xs, np.ascontiguousarray(slots[6:8]), *one)
+    q = np.array([L.orc_quantize_symmetric(float(v), float(one[2][1, 0])) for v in x[7, 0]], np.int8)
+    np.testing.assert_array_equal(one[0][1, 0, 6], q)
+
+
 # ---- paged decode / chunked prefill vs torch float64 on a numpy gather ---------------------------
 def _gather(cache, scales, kv_dtype, table, T, Hq, G, is_v):
     nb, Hkv, B, D = cache.shape
