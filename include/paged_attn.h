@@ -14,8 +14,9 @@
  * caller; the library never frees memory it did not allocate through pa_alloc.
  *
  * Threading: launch functions are asynchronous on the given stream and return after enqueue. The
- * library keeps no mutable global state except a thread-local last-error string, so one pa_device
- * may be driven from several host threads, each with its own stream.
+ * library keeps no mutable global state except a thread-local last-error string and the per-device
+ * scratch array of pa_paged_decode_noalloc, so one pa_device may be driven from several host
+ * threads, each with its own stream (pa_paged_decode_noalloc calls excepted: they share the scratch).
  */
 #ifndef PAGED_ATTN_H
 #define PAGED_ATTN_H
@@ -78,7 +79,7 @@ typedef struct pa_config {
     int32_t block_size;     /* tokens per physical block; 16 in every shipped configuration    */
     int32_t num_q_heads;    /* Hq                                                               */
     int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, query head h reads KV head h / (Hq / Hkv)    */
-    int32_t head_dim;       /* D: 64, 128 or 256                                                */
+    int32_t head_dim;       /* D: 64, 128 or 256; 32 for fp32 / bf16 caches (decode, append)  */
     int32_t kv_dtype;       /* pa_dtype of the cache                                            */
     int32_t q_dtype;        /* pa_dtype of Q and of the new K/V handed to pa_kv_append (FP32/BF16) */
     int32_t num_blocks;     /* physical blocks in the pool; ids outside [0, num_blocks) are
@@ -250,6 +251,23 @@ pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float*
                                  const int32_t* block_tables, const int32_t* context_lens,
                                  int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len,
                                  void* workspace, size_t workspace_bytes);
+
+/* Bytes of device scratch the library holds per device for pa_paged_decode_noalloc. */
+#define PA_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* pa_paged_decode for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation): the same arguments without a workspace; the split-K
+ * partials go to a device array of PA_NOALLOC_SCRATCH_BYTES that the library holds on each device
+ * (resolved at pa_device_open, or at this call's first use on a device) until the process ends.
+ * The call allocates nothing. It returns PA_ERROR_WORKSPACE_TOO_SMALL, launching nothing, when
+ * pa_decode_workspace_size for the same shape exceeds PA_NOALLOC_SCRATCH_BYTES. Every call on a
+ * device shares that device's array: calls that overlap on one device (two streams, two threads)
+ * race. No counterpart in the reference: it serves the callers that cannot allocate. */
+pa_status pa_paged_decode_noalloc(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                  const void* k_cache, const void* v_cache,
+                                  const float* k_scale, const float* v_scale,
+                                  const int32_t* block_tables, const int32_t* context_lens,
+                                  int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len);
 
 /* ---- Shared-prefix decode ----
  * Sequences forked from one parent share the parent's first physical blocks (copy-on-write:

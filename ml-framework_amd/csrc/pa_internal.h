@@ -54,6 +54,10 @@ pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, c
                            void* k_cache, void* v_cache, float* k_scale, float* v_scale, float* k_absmax,
                            float* v_absmax);
 
+// Resolves the device address of pa_paged_decode_noalloc's scratch array on device `ordinal`
+// (paged_decode.hip); pa_device_open calls it once per device.
+pa_status init_decode_scratch(int ordinal);
+
 inline float resolve_scale(const pa_config* cfg) {
     // StandardPagedAttentionKernel.cs:18,28 -- scale > 0 overrides 1/sqrt(headDim).
     return cfg->scale > 0.0f ? cfg->scale : 1.0f / sqrtf(static_cast<float>(cfg->head_dim));

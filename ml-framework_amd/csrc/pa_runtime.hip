@@ -121,6 +121,9 @@ pa_status pa_device_open(int32_t ordinal, pa_device** out_device) {
         return set_error(PA_ERROR_NO_DEVICE, "pa_device_open: no HIP device with ordinal " + std::to_string(ordinal));
     // CudaDevice's constructor makes its device current (HAL/CUDA/CudaDevice.cs:15-21).
     PA_HIP_CHECK(hipSetDevice(ordinal));
+    // Per-device set-up: the scratch address of pa_paged_decode_noalloc.
+    pa_status st = pa::init_decode_scratch(ordinal);
+    if (st != PA_SUCCESS) return st;
     auto* d = new (std::nothrow) pa_device{ordinal};
     if (!d) return set_error(PA_ERROR_OUT_OF_MEMORY, "pa_device_open: host allocation failed");
     *out_device = d;

@@ -15,6 +15,7 @@
 // reduced across lanes with DPP, a partition-wide softmax in LDS, VALU P.V, and the same kind of
 // merge over fixed 256/512-token partitions (paged_decode_merge_kernel).
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -344,6 +345,88 @@ pa_status pa_paged_decode_append(pa_stream* stream, const pa_config* cfg, float*
     return decode_impl("pa_paged_decode_append", true, stream, cfg, out, q, k_new, v_new, k_cache, v_cache,
                        k_scale, v_scale, k_absmax, v_absmax, block_tables, context_lens, num_seqs,
                        max_blocks_per_seq, max_context_len, workspace, workspace_bytes);
+}
+
+}  // extern "C"
+
+// ---- decode without a caller workspace ----
+//
+// pa_paged_decode_noalloc runs pa_paged_decode with the split-K workspace in `scratch`, a
+// file-scope device array of PA_NOALLOC_SCRATCH_BYTES. Every device the library runs on holds its
+// own copy until the process ends; host code reaches a device's copy only through the address
+// hipGetSymbolAddress returns with that device current (kept per device in g_scratch_ptr). The
+// decode reads nothing from the workspace that the same call did not write first, so no clearing
+// is needed; calls that overlap on one device share the array and race.
+
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[PA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on device `ordinal`, resolved once per device.
+pa_status scratch_address(const std::string& f, int ordinal, void** ptr) {
+    if (ordinal < 0 || ordinal >= kMaxScratchDevices)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": device ordinal beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ordinal]) {
+        int prev = -1;
+        PA_HIP_CHECK(hipGetDevice(&prev));
+        if (prev != ordinal) PA_HIP_CHECK(hipSetDevice(ordinal));
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (prev != ordinal) (void)hipSetDevice(prev);
+        if (e != hipSuccess) return pa::set_hip_error(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return pa::set_error(PA_ERROR_HIP, f + ": hipGetSymbolAddress returned a null scratch address");
+        g_scratch_ptr[ordinal] = p;
+    }
+    *ptr = g_scratch_ptr[ordinal];
+    return PA_SUCCESS;
+}
+
+}  // namespace
+
+namespace pa {
+// Called by pa_device_open, the library's per-device set-up.
+pa_status init_decode_scratch(int ordinal) {
+    void* p = nullptr;
+    return scratch_address("pa_device_open", ordinal, &p);
+}
+}  // namespace pa
+
+extern "C" {
+
+pa_status pa_paged_decode_noalloc(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
+                                  const void* k_cache, const void* v_cache, const float* k_scale,
+                                  const float* v_scale, const int32_t* block_tables, const int32_t* context_lens,
+                                  int32_t num_seqs, int32_t max_blocks_per_seq, int32_t max_context_len) {
+    const std::string f = "pa_paged_decode_noalloc";
+    pa_status st = pa::check_config(cfg, f.c_str());
+    if (st != PA_SUCCESS) return st;
+    if (num_seqs < 0 || max_blocks_per_seq < 0 || max_context_len < 0)
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, f + ": negative size");
+    if (num_seqs == 0) return pa::clear_error();
+    std::string err;
+    const int part = resolve_part(cfg, &err);
+    if (part < 0) return pa::set_error(PA_ERROR_UNSUPPORTED, f + ": " + err);
+    // The workspace a pa_paged_decode call of this shape needs (chunks of sequences reuse it).
+    const size_t need = workspace_bytes_for(cfg, num_seqs, effective_max_len(max_context_len, max_blocks_per_seq), part);
+    if (need > PA_NOALLOC_SCRATCH_BYTES)
+        return pa::set_error(PA_ERROR_WORKSPACE_TOO_SMALL,
+                             f + ": this call needs " + std::to_string(need) + " bytes of split-K scratch, above the " +
+                                 std::to_string(static_cast<size_t>(PA_NOALLOC_SCRATCH_BYTES)) +
+                                 " the library holds per device; use pa_paged_decode with a workspace");
+    int ordinal = 0;
+    if (stream) ordinal = stream->ordinal;
+    else PA_HIP_CHECK(hipGetDevice(&ordinal));
+    void* ws = nullptr;
+    st = scratch_address(f, ordinal, &ws);
+    if (st != PA_SUCCESS) return st;
+    return decode_impl(f.c_str(), false, stream, cfg, out, q, nullptr, nullptr, k_cache, v_cache, k_scale, v_scale,
+                       nullptr, nullptr, block_tables, context_lens, num_seqs, max_blocks_per_seq, max_context_len,
+                       ws, PA_NOALLOC_SCRATCH_BYTES);
 }
 
 }  // extern "C"

@@ -52,7 +52,7 @@ EXPORTS = (
     "pa_graph_capture_begin", "pa_graph_capture_end", "pa_graph_launch", "pa_graph_node_count",
     "pa_graph_destroy",
     "pa_build_slot_mapping", "pa_kv_append", "pa_decode_workspace_size", "pa_paged_decode",
-    "pa_paged_decode_append", "pa_chunked_prefill",
+    "pa_paged_decode_append", "pa_paged_decode_noalloc", "pa_chunked_prefill",
     "pa_block_bytes", "pa_copy_blocks", "pa_gather_blocks", "pa_scatter_blocks", "pa_read_block_f32",
     "pa_write_block_f32",
     "pa_qkv_workspace_size", "pa_qkv_project_append", "pa_o_workspace_size", "pa_o_project",
@@ -142,6 +142,7 @@ _SIGNATURES = {
     "pa_paged_decode": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _SZ],
     "pa_paged_decode_append": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                _P, _SZ],
+    "pa_paged_decode_noalloc": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
     "pa_chunked_prefill": [_P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32],
     "pa_prefix_plan_bytes": [_I32, ctypes.POINTER(_SZ)],
     "pa_prefix_plan_build": [_P, _CFG, _I32, _P, _P, _SZ, ctypes.POINTER(_I32)],
@@ -345,6 +346,13 @@ def paged_decode_append(stream, cfg: PaConfig, out, q, k_new, v_new, k_cache, v_
          _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
          _ptr(k_absmax), _ptr(v_absmax), _ptr(block_tables), _ptr(context_lens), num_seqs,
          max_blocks_per_seq, max_context_len, _ptr(workspace), workspace_bytes)
+
+
+def paged_decode_noalloc(stream, cfg: PaConfig, out, q, k_cache, v_cache, k_scale, v_scale, block_tables,
+                         context_lens, num_seqs, max_blocks_per_seq, max_context_len):
+    call("pa_paged_decode_noalloc", stream.handle if stream else None, ctypes.byref(cfg), _ptr(out), _ptr(q),
+         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_tables), _ptr(context_lens),
+         num_seqs, max_blocks_per_seq, max_context_len)
 
 
 def prefix_plan_bytes(num_seqs: int) -> int:
