@@ -43,6 +43,10 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) written |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(written), o, 64));
     const bool fresh = (written & 1u) != 0;
+    const int64_t sidx = blk * num_kv_heads + h;
+    // The block's statistics are loaded with the segment's values (one round trip for both).
+    const float amax_mem = have_stats ? 0.0f : absmax[sidx];
+    const float scale_mem = have_stats ? 0.0f : scale[sidx];
     float seg_amax = 0.0f;
     for (int t = s; t < e; t++) {
         const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
@@ -54,7 +58,6 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
     }
     seg_amax = wave_max(seg_amax);
 
-    const int64_t sidx = blk * num_kv_heads + h;
     int8_t* block_codes = cache + ((blk * num_kv_heads + h) * kBlockSize) * D;
     // Element (row off, dim d) of the tile: K is [16][D], V is [D][16].
     auto at = [&](int off, int d) -> int8_t* {
@@ -70,8 +73,8 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
         }
     } else {
         if (!have_stats) {
-            amax = absmax[sidx];
-            cur_scale = scale[sidx];
+            amax = amax_mem;
+            cur_scale = scale_mem;
         }
         if (seg_amax > amax) {
             const float old_scale = cur_scale;

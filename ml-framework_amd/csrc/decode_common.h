@@ -383,11 +383,17 @@ __device__ __forceinline__ s16x4_t v_operand(const uint32_t& r) {
 }
 
 // First of the 8 consecutive dims of K slab sl (32 dims of one QK MFMA) that lane group q4 feeds
-// in the decode kernel: the dot product does not depend on which dims go to which MFMA k slot as
-// long as K and Q agree, so each lane group takes a contiguous D / 4 dims over its slabs and its
-// piece of a K row is one run (two 16-byte loads for int8 D 128 instead of four 8-byte ones).
-template <int D>
-__device__ __forceinline__ int k_dim0(int sl, int q4) { return (D / 4) * q4 + 8 * sl; }
+// in the decode kernel. The dot product does not depend on which dims go to which MFMA k slot as
+// long as K and Q agree, so the choice is made for the loads:
+//  - bf16: slab sl, lane group q4 -> dims 32 sl + 8 q4 (bytes 64 sl + 16 q4 of the row): one K
+//    load instruction reads 64 contiguous bytes of each of 16 rows (timed equal to a contiguous
+//    quarter of the dims per lane group, whose pieces land on both lines of each row);
+//  - int8: a contiguous quarter of the dims per lane group, so a lane's piece of a K row is two
+//    16-byte loads instead of four 8-byte ones (each instruction still covers 16 lines).
+template <int D, int KV>
+__device__ __forceinline__ int k_dim0(int sl, int q4) {
+    return KV == PA_DTYPE_INT8 ? (D / 4) * q4 + 8 * sl : 32 * sl + 8 * q4;
+}
 
 // ---- fused append: the new token (row r of the sequence's last block) enters the owning wave's
 // registers and the cache. Values and cache bytes are those of pa_kv_append for that one token.
@@ -407,7 +413,7 @@ __device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t ti
     if (n == r) {  // K row r: dims 32s + 8q4 .. +8 of this lane
 #pragma unroll
         for (int sl = 0; sl < NSLAB; sl++) {
-            const int d0 = k_dim0<D>(sl, q4);
+            const int d0 = k_dim0<D, PA_DTYPE_BF16>(sl, q4);
             const float* x = s_new + d0;
             const uint4 v = make_uint4(pack_bf16_trunc(x[0], x[1]), pack_bf16_trunc(x[2], x[3]),
                                        pack_bf16_trunc(x[4], x[5]), pack_bf16_trunc(x[6], x[7]));

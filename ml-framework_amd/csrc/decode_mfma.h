@@ -20,7 +20,8 @@
 //
 // Per block: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads padded
 // to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
-// split into bf16 high and low parts (~16 significant bits). The score layout the first MFMA
+// split into bf16 high and low parts (~16 significant bits) for bf16 caches, one rounded bf16 P for
+// int8 caches. The score layout the first MFMA
 // leaves in registers (lane = (token group q4, head n)) is the A-operand layout of the second, so
 // P never leaves registers. Three rotating register buffers keep two blocks in flight while a
 // third is consumed.
@@ -61,6 +62,12 @@ struct Piece {
 };
 
 constexpr int kPieceBlocks = 64;  // one block id per lane
+
+// Register buffers of a wave's block pipeline (blocks in flight + the one being consumed).
+#ifndef PA_INT8_DECODE_BUFFERS
+#define PA_INT8_DECODE_BUFFERS 3
+#endif
+__host__ __device__ constexpr int decode_buffers(int kv) { return kv == PA_DTYPE_INT8 ? PA_INT8_DECODE_BUFFERS : 3; }
 
 // Ids of a piece's blocks: lane j holds block b0 + j (-1 beyond the piece). Ids are range-checked
 // where they are used (valid_bid): a check here would make the wave wait for the table load at the
@@ -186,7 +193,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             float x[NSLAB][8];
 #pragma unroll
             for (int s = 0; s < NSLAB; s++) {
-                const int d0 = k_dim0<D>(s, q4);
+                const int d0 = k_dim0<D, KV>(s, q4);
                 if constexpr (QF32) {
                     const float* qp = static_cast<const float*>(a.q) + qrow + d0;
 #pragma unroll
@@ -204,7 +211,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         } else {
 #pragma unroll
         for (int s = 0; s < NSLAB; s++) {
-            const int d0 = k_dim0<D>(s, q4);
+            const int d0 = k_dim0<D, KV>(s, q4);
             if constexpr (QF32) {
                 const float* qp = static_cast<const float*>(a.q) + qrow + d0;
                 float x[8];
@@ -256,7 +263,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     const char* vc = static_cast<const char*>(a.v_cache);
     using KR = typename Raw::K;
     using VR = typename Raw::V;
-    const int k_lane_off = (n * D + k_dim0<D>(0, q4)) * ELT;  // K row n, D / 4 dims from here
+    const int k_row_off = n * D * ELT;  // K row n; slab s of this lane starts at dim k_dim0(s, q4)
     constexpr int kLoadCP = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
     const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
     // Loads go through per-block buffer descriptors: a block past the wave's list or with an
@@ -274,13 +281,14 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
 #pragma unroll
             for (int s = 0; s < NSLAB; s += 2) {
-                const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_lane_off + 8 * s);
+                const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4));
                 kr[s] = make_uint2(w.x, w.y);
                 kr[s + 1] = make_uint2(w.z, w.w);
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kLoadCP>(rk, k_lane_off + 8 * s * ELT);
+            for (int s = 0; s < NSLAB; s++)
+                kr[s] = buffer_load<KR, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
         }
 #pragma unroll
         for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kLoadCP>(rv, v_lane_off + 256 * t * ELT);
@@ -378,26 +386,61 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             l_run += p[i];
             if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
         }
-        uint32_t hi[2], lo[2];
+        if constexpr (KV == PA_DTYPE_INT8) {
+            // int8 caches (bar 2e-2): one bf16 P, rounded to nearest (relative error <= 2^-9),
+            // half the PV MFMAs of the split below. p is finite and non-negative.
+            uint32_t pr[2];
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const float a0 = p[2 * e], a1 = p[2 * e + 1];
-            const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
-            const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
-            hi[e] = pack_bf16_trunc(a0, a1);
-            lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
-        }
-        const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
-        const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+            for (int e = 0; e < 2; e++) {
+                const uint32_t b0 = __float_as_uint(p[2 * e]), b1 = __float_as_uint(p[2 * e + 1]);
+                pr[e] = pack_bf16_trunc(__uint_as_float(b0 + 0x7fffu + ((b0 >> 16) & 1u)),
+                                        __uint_as_float(b1 + 0x7fffu + ((b1 >> 16) & 1u)));
+            }
+            const s16x4_t pb = __builtin_bit_cast(s16x4_t, make_uint2(pr[0], pr[1]));
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const s16x4_t vop = v_operand(vr[t]);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+            for (int t = 0; t < NT; t++)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pb, v_operand(vr[t]), acc[t], 0, 0, 0);
+        } else {
+            uint32_t hi[2], lo[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float a0 = p[2 * e], a1 = p[2 * e + 1];
+                const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
+                const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
+                hi[e] = pack_bf16_trunc(a0, a1);
+                lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+            }
+            const s16x4_t phi = __builtin_bit_cast(s16x4_t, make_uint2(hi[0], hi[1]));
+            const s16x4_t plo = __builtin_bit_cast(s16x4_t, make_uint2(lo[0], lo[1]));
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const s16x4_t vop = v_operand(vr[t]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vop, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vop, acc[t], 0, 0, 0);
+            }
         }
     };
 
-    {
+    if constexpr (decode_buffers(KV) != 3) {
+        // NB rotating register buffers: NB - 1 blocks in flight while one is consumed (int8 blocks
+        // carry half the bytes of bf16 ones, so more of them are kept in flight).
+        constexpr int NB = decode_buffers(KV);
+        KR kbuf[NB][NSLAB];
+        VR vbuf[NB][NT];
+#pragma unroll
+        for (int i = 0; i < NB - 1; i++) load(kbuf[i], vbuf[i], i);
+        prefetch_next();
+        side_loads();
+        int j = 0;
+        while (j < nb) {
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                load(kbuf[(b + NB - 1) % NB], vbuf[(b + NB - 1) % NB], j + NB - 1);
+                compute(kbuf[b], vbuf[b], j, false);
+                if (++j >= nb) break;
+            }
+        }
+    } else {
         // Three rotating register buffers: two blocks in flight while a third is consumed. Loads
         // past the wave's list are zero-sized (no memory traffic), so they are issued regardless.
         KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
@@ -590,7 +633,15 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     const int64_t W = a.split_grid;
     const int64_t C = split_range_blocks(a, total);
     const int64_t units = (total + C - 1) / C * Hkv;
-    int64_t u = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+    // int8 caches: workgroup b runs on XCD b % 8, and consecutive logical workgroups are placed on
+    // one XCD, so the KV heads of a range (and neighbouring ranges) are read from one L2 at about
+    // the same time (C4 134.8 -> 132.2 us; bf16 caches measured slower with it, 53.3 -> 54.9 us).
+    int lb = static_cast<int>(blockIdx.x);
+    if constexpr (KV == PA_DTYPE_INT8) {
+        const int nwg = static_cast<int>(gridDim.x);
+        if (nwg % 8 == 0) lb = static_cast<int>((blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8);
+    }
+    int64_t u = static_cast<int64_t>(lb) * WAVES + wave;
     if (u >= W || u >= units) return;
     int64_t r = u / Hkv;
     int kvh = static_cast<int>(u - r * Hkv);

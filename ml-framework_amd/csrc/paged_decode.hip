@@ -137,7 +137,13 @@ __global__ __launch_bounds__(pa::kAppendMaxThreads) void append_last_token_int8_
         const int32_t bid = a.block_tables[static_cast<int64_t>(t) * a.max_blocks_per_seq + (T - 1) / pa::kBlockSize];
         return bid >= 0 ? static_cast<int64_t>(bid) * pa::kBlockSize + (T - 1) % pa::kBlockSize : -1;
     };
-    pa::append_int8_block<D>(a.k_new, a.v_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D, last_slot,
+    // Every sequence's slot, looked up once by the workgroup (two dependent loads each, all in
+    // flight together): the owner's scans then read LDS.
+    __shared__ int64_t s_slot[pa::kMaxPersistentSeqs];
+    for (int t = threadIdx.x; t < num_seqs; t += blockDim.x) s_slot[t] = last_slot(t);
+    __syncthreads();
+    auto slot_at = [&](int t) -> int64_t { return s_slot[t]; };
+    pa::append_int8_block<D>(a.k_new, a.v_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D, slot_at,
                              static_cast<int32_t>(blockIdx.x), num_seqs,
                              static_cast<int8_t*>(const_cast<void*>(a.k_cache)),
                              static_cast<int8_t*>(const_cast<void*>(a.v_cache)), const_cast<float*>(a.k_scale),
