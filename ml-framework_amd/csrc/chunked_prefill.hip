@@ -15,8 +15,8 @@
 // loads its 16-byte pieces of the pair's K and V tiles into registers one step ahead, writes
 // them into one of two LDS slots, and after one barrier every wave reads its MFMA operands from
 // that slot, so a K/V tile crosses from memory once per workgroup. The LDS tiles are stored with
-// an XOR swizzle of 16-byte chunks (and the pair's second tile offset by half a bank line) so the
-// operand reads are free of bank conflicts. Per pair of blocks and unit:
+// XOR swizzles of 16-byte chunks (and the pair's second tile a quarter of a bank line further) so
+// the bf16 operand reads are free of bank conflicts. Per pair of blocks and unit:
 // S^T[32 keys][16 queries] = K . Q^T on two v_mfma_f32_16x16x32_bf16 per 32 dims, whose rows are
 // permuted so every lane ends up with 8 consecutive keys of one block; online softmax per query
 // in fp32 (log2 domain, rescale only past a 2^12 margin, mask only on the pairs at the causal
@@ -61,28 +61,39 @@ constexpr int kPrefillThreads = 64 * kPrefillWaves;
 constexpr int kPrefillUnits = 2 * kPrefillWaves;  // units per workgroup round
 
 // LDS geometry of one staged block (K tile then V tile) for head_dim D and element size ELT.
+// gfx950's LDS serves 256 bytes a clock (64 banks of 4 bytes). A 16-byte read (ds_read_b128) of a
+// wave takes 4 clocks of 16 lanes each, the lanes of one clock being the quads (4 consecutive
+// lanes) of one half-wave whose quad index (0..7) has the same bit parity: {0, 3, 5, 6} and
+// {1, 2, 4, 7}. Two lanes of one clock on the same 16-byte position of a 256-byte line (at
+// different addresses) cost a clock more. The layouts below give each clock 16 distinct positions.
 template <int D, int ELT> struct PrefillTile {
     static constexpr int RC = D * ELT / 16;             // 16-byte chunks per K row
     static constexpr int K_CHUNKS = 16 * RC;             // K tile [16][D]
     static constexpr int VRC = ELT;                      // 16-byte chunks per V row (16 tokens)
     static constexpr int CHUNKS = 2 * K_CHUNKS;          // K + V tiles, same size
-    static constexpr int BYTES = CHUNKS * 16;
     static constexpr int KP = (K_CHUNKS + kPrefillThreads - 1) / kPrefillThreads;  // per-thread chunks of each tile
     static constexpr int PER_THREAD = 2 * KP;          // K chunks first, then V chunks
-    // K row r's chunk c is stored at chunk r * RC + (c ^ kx(r)). One QK operand read (8 lanes)
-    // takes one chunk column of 4 consecutive rows in each of the pair's two tiles, whose bases
-    // differ by half a 128-byte bank line: kx spreads the 4 rows over the other 2 bits of the
-    // line's 8 chunk positions. It only touches the chunk index's low 2 bits (the lane group's
-    // part), so the slab part stays an immediate offset.
-    __device__ static constexpr int kx(int r) { return r & 3; }
+    // K row r's chunk c is stored at chunk r * RC + kswz(r, c). A QK operand read takes one chunk
+    // column c = 4 sl + q4 (q4 = lane / 16) of rows (n & 3) + 8 (n >> 3) (+ 4) of tile (n >> 2) & 1
+    // (n = lane % 16); the second tile sits 4 positions further. In one clock, lane groups q4 and
+    // q4 ^ 1 meet with 2 quads each, one of each tile: the low 2 bits (row & 3) separate the lanes of
+    // a quad, and the quads get distinct high 2 bits from the tile offset plus, for bf16 rows of 16
+    // or more chunks, bit 3 flipped by the column's bit 0 (q4 & 1); 128-byte rows (D = 64) get that
+    // spread from the row parity. int8 keeps the row-only swizzle.
+    __device__ static constexpr int kswz(int r, int c) {
+        return c ^ (r & 3) ^ (ELT == 2 && RC >= 16 ? (c & 1) << 3 : 0);
+    }
+    __device__ static constexpr int kpos(int r, int c) { return r * RC + kswz(r, c); }
     // Chunk offset of block b of slot `slot` in the LDS ring: block 1 sits 4 chunks (64 bytes)
-    // further, so equal positions in the two tiles fall in opposite halves of a bank line.
+    // further, a quarter of a bank line.
     static constexpr int SLOT = 2 * CHUNKS + 8;
     __device__ static constexpr int base(int slot, int b) { return slot * SLOT + b * (CHUNKS + 4); }
-    // LDS chunk of V row d, half h. A PV operand read takes one half of 8 consecutive rows; bf16
-    // rows are 2 chunks, and rows 4..7 of each 8 swap halves so the 8 reads hit 8 distinct positions.
-    __device__ static constexpr int vpos(int d, int h) { return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ ((d >> 2) & 1)) : h); }
-
+    // LDS chunk of V row d, half h, in block b of the pair. A bf16 PV operand read takes half
+    // q4 >> 1 of 8 consecutive rows from each tile (b = q4 & 1) in one clock: the half stored first
+    // is h ^ b, so the two tiles' rows land on even and odd positions.
+    __device__ static constexpr int vpos(int d, int h, int b) {
+        return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ b) : h);
+    }
 };
 
 // Work units are (16-query tile, query head) pairs of one KV head. A workgroup takes QT =
@@ -144,19 +155,16 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
     // This thread's chunks of a block: entry k < KP is a K chunk, the others V chunks (so each
     // load uses one descriptor for the whole wave); byte offset within the tile (past the end for a
     // thread without a chunk: such loads return zeros) and LDS chunk.
-    int g_off[PT], l_pos[PT];
+    int g_off[PT], l_pos[2][PT];  // l_pos[b]: LDS chunk within block b of the pair
     bool live[PT];
 #pragma unroll
     for (int k = 0; k < PT; k++) {
         const int c = tid + kPrefillThreads * (k % TL::KP);
         live[k] = c < TL::K_CHUNKS;
         g_off[k] = live[k] ? c * 16 : TILE * ELT;
-        if (k < TL::KP) {
-            const int r = c / TL::RC, cc = c % TL::RC;
-            l_pos[k] = r * TL::RC + (cc ^ TL::kx(r));
-        } else {
-            l_pos[k] = TL::vpos(c / TL::VRC, c % TL::VRC);
-        }
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+            l_pos[b][k] = k < TL::KP ? TL::kpos(c / TL::RC, c % TL::RC) : TL::vpos(c / TL::VRC, c % TL::VRC, b);
     }
     // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS: reading them there
     // costs no wait on the streaming loads (a table load inside the stream would).
@@ -185,7 +193,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
         for (int b = 0; b < 2; b++)
 #pragma unroll
             for (int k = 0; k < PT; k++)
-                if (live[k]) s_tile[TL::base(slot, b) + l_pos[k]] = st[b][k];
+                if (live[k]) s_tile[TL::base(slot, b) + l_pos[b][k]] = st[b][k];
     };
 
     const int U = QT * G;
@@ -269,10 +277,10 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                 for (int sl = 0; sl < NSLAB; sl++) {
                     if constexpr (ELT == 2) {  // 8 bf16 = one 16-byte chunk
                         const int cc = 4 * sl + q4;
-                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + (r * TL::RC + (cc ^ TL::kx(r))) * 16));
+                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + TL::kpos(r, cc) * 16));
                     } else {  // 8 int8 codes = half a chunk
                         const int cc = 2 * sl + (q4 >> 1);
-                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + (r * TL::RC + (cc ^ TL::kx(r))) * 16 + (q4 & 1) * 8));
+                        kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + TL::kpos(r, cc) * 16 + (q4 & 1) * 8));
                     }
                 }
 #pragma unroll
@@ -367,8 +375,8 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
             for (int t = 0; t < NT; t++) {
                 const int d = 16 * t + n;
                 bf16x8_t vop;
-                if constexpr (ELT == 2) vop = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1) * 16));
-                else vop = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0) * 16 + (q4 >> 1) * 8));
+                if constexpr (ELT == 2) vop = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
+                else vop = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0, pblk) * 16 + (q4 >> 1) * 8));
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
                     acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[k], vop, acc[k][t], 0, 0, 0);
