@@ -11,10 +11,10 @@
 // Work decomposition: the units are (16-query tile, query head) pairs of one KV head. A
 // workgroup of 4 waves takes 2 (G = 4) or more consecutive query tiles of one (sequence, KV head)
 // -- all of them on one XCD, the heaviest first -- and each wave computes two units on the same
-// K/V operands. The workgroup streams the key blocks through LDS two at a time: each thread
-// loads its 16-byte pieces of the pair's K and V tiles into registers one step ahead, writes
-// them into one of two LDS slots, and after one barrier every wave reads its MFMA operands from
-// that slot, so a K/V tile crosses from memory once per workgroup. The LDS tiles are stored with
+// K/V operands. The workgroup streams the key blocks through LDS two at a time: the pair's K and
+// V tiles go from memory straight into one of three LDS slots (16-byte buffer loads with the LDS
+// bit, issued two pairs ahead), and after one barrier every wave reads its MFMA operands from
+// that slot, so a K/V tile crosses from memory once per workgroup and never through registers. The LDS tiles are stored with
 // XOR swizzles of 16-byte chunks (and the pair's second tile a quarter of a bank line further) so
 // the bf16 operand reads are free of bank conflicts. Per pair of blocks and unit:
 // S^T[32 keys][16 queries] = K . Q^T on two v_mfma_f32_16x16x32_bf16 per 32 dims, whose rows are
@@ -71,8 +71,7 @@ template <int D, int ELT> struct PrefillTile {
     static constexpr int K_CHUNKS = 16 * RC;             // K tile [16][D]
     static constexpr int VRC = ELT;                      // 16-byte chunks per V row (16 tokens)
     static constexpr int CHUNKS = 2 * K_CHUNKS;          // K + V tiles, same size
-    static constexpr int KP = (K_CHUNKS + kPrefillThreads - 1) / kPrefillThreads;  // per-thread chunks of each tile
-    static constexpr int PER_THREAD = 2 * KP;          // K chunks first, then V chunks
+    static constexpr int SPT = K_CHUNKS / 64;            // 64-chunk segments (one wave's load) per tile
     // K row r's chunk c is stored at chunk r * RC + kswz(r, c). A QK operand read takes one chunk
     // column c = 4 sl + q4 (q4 = lane / 16) of rows (n & 3) + 8 (n >> 3) (+ 4) of tile (n >> 2) & 1
     // (n = lane % 16); the second tile sits 4 positions further. In one clock, lane groups q4 and
@@ -84,6 +83,12 @@ template <int D, int ELT> struct PrefillTile {
         return c ^ (r & 3) ^ (ELT == 2 && RC >= 16 ? (c & 1) << 3 : 0);
     }
     __device__ static constexpr int kpos(int r, int c) { return r * RC + kswz(r, c); }
+    // Memory chunk of the K tile stored at LDS position p (the inverse of kpos).
+    __device__ static constexpr int ksrc(int p) {
+        const int r = p / RC, x = p % RC;
+        const int c0 = (x ^ r) & 1;  // bit 0 of the column (kswz keeps it up to the row's bit 0)
+        return r * RC + (x ^ (r & 3) ^ (ELT == 2 && RC >= 16 ? c0 << 3 : 0));
+    }
     // Chunk offset of block b of slot `slot` in the LDS ring: block 1 sits 4 chunks (64 bytes)
     // further, a quarter of a bank line.
     static constexpr int SLOT = 2 * CHUNKS + 8;
@@ -94,7 +99,36 @@ template <int D, int ELT> struct PrefillTile {
     __device__ static constexpr int vpos(int d, int h, int b) {
         return K_CHUNKS + d * VRC + (VRC == 2 ? (h ^ b) : h);
     }
+    // Memory chunk of block b's V tile stored at position p of the V area (the inverse of vpos).
+    __device__ static constexpr int vsrc(int p, int b) { return VRC == 2 ? p ^ b : p; }
 };
+
+// 16 bytes per lane from a buffer into LDS: lane l's bytes land at LDS address lds + 16 l
+// (buffer_load_dwordx4 with the LDS bit; M0 holds the LDS address, and one wait state must
+// separate the M0 write from the load; M0 is restored afterwards). A zero-sized descriptor
+// writes zeros. Written as inline asm so that the compiler, which does not see these LDS
+// writes, adds no wait on them before its own LDS reads: the kernel orders them itself (vmcnt
+// wait + barrier per step). The LDS address is an operand and the asm clobbers memory, so the
+// compiler treats the array as written by it.
+using u32x4_t = uint32_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_load16(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %1, 0 offen lds\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(rsrc), "v"(voffset), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ u32x4_t buffer_rsrc_words(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
+                   static_cast<uint32_t>(kBufferFlags)};
+}
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    using lds_char = const __attribute__((address_space(3))) char;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)p));  // generic -> LDS offset
+}
 
 // Work units are (16-query tile, query head) pairs of one KV head. A workgroup takes QT =
 // max(1, kPrefillUnits / G) consecutive query tiles, i.e. QT * G units, kPrefillUnits at a time:
@@ -109,9 +143,10 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
     constexpr int TILE = 16 * D;
     using KR = typename Raw::K;
     using TL = PrefillTile<D, ELT>;
-    constexpr int PT = TL::PER_THREAD;
-    constexpr int R = 1;  // block pairs in flight (register staging): 1 or 2
-    __shared__ __align__(16) uint4 s_tile[2 * TL::SLOT];  // 2 slots x 2 blocks (TL::base)
+    constexpr int NSLOT = 3;  // LDS slots: the pair being computed and two in flight
+    constexpr int NSEG = 4 * TL::SPT / kPrefillWaves;  // 64-chunk loads per wave per pair (4 tiles)
+    static_assert((4 * TL::SPT) % kPrefillWaves == 0, "a pair's tiles must split evenly over the waves");
+    __shared__ __align__(16) uint4 s_tile[NSLOT * TL::SLOT];  // NSLOT slots x 2 blocks (TL::base)
 
     // Workgroup -> (query-tile group, KV head, sequence). Workgroup ids are dispatched to the 8
     // XCDs in turn (id mod 8); every query-tile group of (sequence, KV head) group gi runs on XCD
@@ -152,48 +187,36 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
     const char* kc = static_cast<const char*>(a.k_cache);
     const char* vc = static_cast<const char*>(a.v_cache);
 
-    // This thread's chunks of a block: entry k < KP is a K chunk, the others V chunks (so each
-    // load uses one descriptor for the whole wave); byte offset within the tile (past the end for a
-    // thread without a chunk: such loads return zeros) and LDS chunk.
-    int g_off[PT], l_pos[2][PT];  // l_pos[b]: LDS chunk within block b of the pair
-    bool live[PT];
+    // This wave's loads of a pair: segment k is 64-chunk segment wave + 4k of the pair's tiles
+    // (block 0 K, block 0 V, block 1 K, block 1 V). Lane l fills LDS position s0 + l of its tile
+    // and therefore loads the memory chunk the layout puts there.
+    int seg_off[NSEG];  // byte offset of this lane's chunk in its tile's memory
 #pragma unroll
-    for (int k = 0; k < PT; k++) {
-        const int c = tid + kPrefillThreads * (k % TL::KP);
-        live[k] = c < TL::K_CHUNKS;
-        g_off[k] = live[k] ? c * 16 : TILE * ELT;
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-            l_pos[b][k] = k < TL::KP ? TL::kpos(c / TL::RC, c % TL::RC) : TL::vpos(c / TL::VRC, c % TL::VRC, b);
+    for (int k = 0; k < NSEG; k++) {
+        const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT, b = t >> 1;
+        const int pos = (sg % TL::SPT) * 64 + lane;
+        seg_off[k] = 16 * ((t & 1) ? TL::vsrc(pos, b) : TL::ksrc(pos));
     }
-    // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS: reading them there
-    // costs no wait on the streaming loads (a table load inside the stream would).
+    // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS.
     constexpr int KCH = 1024;
     __shared__ int s_ids[KCH];
     __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1];
-    // Loads of a block into staging registers through per-block buffer descriptors: an invalid
-    // block or one past the end gets zero-sized descriptors and reads as zeros. The loads are the
-    // same on every step (no branches), so each wait is for exactly the block it needs.
-    auto stage = [&](uint4 (&st)[2][PT], int jl, int nkc) {  // blocks jl, jl + 1
+    const uint32_t tile_lds = lds_address(s_tile);
+    // Loads of the pair of blocks jl, jl + 1 (of the current chunk of the table) into slot `slot`.
+    // A block past the chunk or with an invalid id gets a zero-sized descriptor and reads as zeros,
+    // so every wave issues the same NSEG loads per pair and one vmcnt value covers them all.
+    auto issue = [&](int jl, int nkc, int slot) {
+        const int id0 = __builtin_amdgcn_readfirstlane(jl < nkc ? s_ids[jl] : -1);
+        const int id1 = __builtin_amdgcn_readfirstlane(jl + 1 < nkc ? s_ids[jl + 1] : -1);
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int bid = jl + b < nkc ? s_ids[jl + b] : -1;
+        for (int k = 0; k < NSEG; k++) {
+            const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT, b = t >> 1;
+            const int bid = b ? id1 : id0;
             const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
-            const int bytes = bid >= 0 ? TILE * ELT : 0;
-            const __amdgpu_buffer_rsrc_t rk =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
-            const __amdgpu_buffer_rsrc_t rv =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
-#pragma unroll
-            for (int k = 0; k < PT; k++) st[b][k] = buffer_load<uint4>(k < TL::KP ? rk : rv, g_off[k]);
+            const u32x4_t rsrc = buffer_rsrc_words(((t & 1) ? vc : kc) + tile, bid >= 0 ? TILE * ELT : 0);
+            const int lpos = TL::base(slot, b) + ((t & 1) ? TL::K_CHUNKS : 0) + (sg % TL::SPT) * 64;
+            lds_load16(rsrc, seg_off[k], tile_lds + 16 * lpos);
         }
-    };
-    auto publish = [&](const uint4 (&st)[2][PT], int slot) {
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-#pragma unroll
-            for (int k = 0; k < PT; k++)
-                if (live[k]) s_tile[TL::base(slot, b) + l_pos[b][k]] = st[b][k];
     };
 
     const int U = QT * G;
@@ -246,6 +269,9 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
             }
         }
 
+        // The Q loads land here, once, rather than behind a wait inside the stream loop (the
+        // compiler does not count the slot loads, so it cannot tell them apart there).
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         float m_run[2] = {-INFINITY, -INFINITY};  // log2 units, query n
         float l_run[2] = {0.0f, 0.0f};            // int8: sum of P for query n over this lane's keys
         f32x4_t acc_l[2], acc[2][NT];             // bf16: row sums of P; outputs (queries 4q4 + i)
@@ -392,20 +418,19 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
             }
         };
 
-        // Stream, a pair of blocks per step: pair j (blocks 2j, 2j + 1 of the chunk) is published
-        // into slot j % 2 at step j (its staging registers were loaded R steps earlier), the
-        // registers are refilled with pair j + R, one barrier, then every wave computes pair j.
-        // Slot j % 2 was last read by compute(j - 2), which every wave finished before the
-        // barrier of step j - 1. Whole rounds of 2 steps keep the slot and the staging registers'
-        // indices static; a step past the end publishes and stages zeros and computes with every
-        // key masked (harmless, and the loads and the compute stay the same on every step: a
-        // branch around the compute would make the accumulators change registers).
+        // Stream, a pair of blocks per step: pair j (blocks 2j, 2j + 1 of the chunk) was loaded
+        // into slot j % 3 two steps earlier. Step j waits until this wave's loads of pair j are
+        // done (at most pair j + 1's NSEG loads outstanding; loads complete in order), ends its
+        // LDS reads, and meets the other waves at a barrier; then it loads pair j + 2 into slot
+        // (j + 2) % 3, whose last reader, compute(j - 1), every wave has finished, and computes
+        // pair j. Loads past the chunk's end write zeros into slots nobody reads.
         for (int c0 = 0; c0 < nkb; c0 += KCH) {
             const int nkc = min(KCH, nkb - c0);
             const int npair = (nkc + 1) / 2;
             const int kend = (c0 + nkc) * 16;        // keys of this chunk of the table end here
             const int kend_lo = min(klim_lo, kend);  // pairs reaching past it need the mask
-            __syncthreads();  // the previous chunk's ids and the slots are no longer read
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's slot loads have landed
+            __syncthreads();  // the previous chunk's ids and the slots are no longer read or written
             for (int i = tid; i < nkc; i += kPrefillThreads) {
                 int id = table[c0 + i];
                 id = id < a.num_blocks ? id : -1;
@@ -422,21 +447,20 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                 }
             }
             __syncthreads();
-            uint4 stg[R][2][PT];
-#pragma unroll
-            for (int r = 0; r < R; r++) stage(stg[r], 2 * r, nkc);
-            for (int j0 = 0; j0 < npair; j0 += 2) {
-#pragma unroll
-                for (int u = 0; u < 2; u++) {  // u = the slot, so LDS offsets are static
-                    const int jp = j0 + u;
-                    publish(stg[u % R], u);
-                    stage(stg[u % R], 2 * (jp + R), nkc);
-                    __syncthreads();
-                    const int lb = c0 + 2 * jp;
-                    compute((lb + 2) * 16 > kend_lo, kend, u, lb, 2 * jp);
-                }
+            issue(0, nkc, 0);
+            issue(2, nkc, 1);
+            int slot = 0, load_slot = 2;  // slots of pair jp and of pair jp + 2
+            for (int jp = 0; jp < npair; jp++) {
+                static_assert(NSEG <= 15, "vmcnt immediate");
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(NSEG) : "memory");
+                issue(2 * (jp + 2), nkc, load_slot);
+                const int lb = c0 + 2 * jp;
+                compute((lb + 2) * 16 > kend_lo, kend, slot, lb, 2 * jp);
+                slot = slot == NSLOT - 1 ? 0 : slot + 1;
+                load_slot = load_slot == NSLOT - 1 ? 0 : load_slot + 1;
             }
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // the slots are reused by the next round
 
         // rows of acc are queries 4q4 + i (int8: their sums live in lanes n = 4q4 + i)
