@@ -7,6 +7,10 @@ blocks): append the new token's K/V of every sequence into the paged cache and a
 sequence's whole context, as one pa_paged_decode_append call (the fused decode kernel plus the
 split-K merge). Inputs are resident in HBM before timing starts; all launches go through the
 C-ABI of libpa_hip.so on one pa_stream and are timed with pa_events recorded on that stream.
+The timed steps alternate between two disjoint copies of the cache (about 2 x 300 MB), so no step
+finds K/V that the step before left in the 256 MB last-level cache: the figure is the cold-HBM
+rate a serving loop sees when the other layers' K/V pass through that cache between two steps of
+one layer. The same step repeated over one pool is reported beside it as `one_pool`.
 
 Output: one JSON line. `value` is the achieved algorithmic HBM bandwidth of the whole step
 (distinct KV bytes read + Q + O + block tables + the appended K/V, divided by the step time);
@@ -175,6 +179,30 @@ def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
            "step": "pa_paged_decode_append" if fused else "pa_paged_decode"}
     del inp, out, ws
     return res
+
+
+def run_two_pool(w, inp, timer, stream, cfg, steps, warmup):
+    """The headline step alternating between two disjoint copies of the C2 cache (same tables, a
+    second pool in its own memory): a pair of steps touches about twice the 256 MB last-level
+    cache, so no step finds its K/V left in that cache by the step before. Returns (ms per step,
+    summary)."""
+    inp2 = make_inputs(w, seed=4321)
+    out, ws, wsb = decode_buffers(w, cfg)
+    s1 = decode_step(w, inp, stream, cfg, True, out, ws, wsb)
+    s2 = decode_step(w, inp2, stream, cfg, True, out, ws, wsb)
+
+    def pair():
+        s1()
+        s2()
+
+    ms = timer(pair, max(1, steps // 2), warmup) / 2
+    nbytes = w.decode_algorithmic_bytes() + append_bytes(w)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    res = {"us_per_layer_step": round(ms * 1e3, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+           "kv_bytes_per_pool": int(2 * inp["k_cache"].numel() * inp["k_cache"].element_size()),
+           "step": "pa_paged_decode_append, pools alternating"}
+    del inp2, out, ws
+    return ms, res
 
 
 def run_prefix_decode(w, timer, stream, steps, warmup, seed):
@@ -438,6 +466,23 @@ def run_layer(timer, stream, w, inp, steps, warmup, seed):
             "o_weight_gbps": round(wo_bytes / (t["o"] * 1e-6) / 1e9, 1), "layer_us": round(t["layer"], 2)}
 
 
+def copy_calibration(args, stream):
+    """10 plain device-to-device copies of --copy-calibration-mb MiB (pa_memcpy): the reference
+    dispatches for scaling hardware byte counters (FETCH_SIZE, WRITE_SIZE) in the same process."""
+    import torch
+
+    if args.copy_calibration_mb <= 0:
+        return
+    nbytes = args.copy_calibration_mb << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    torch.cuda.synchronize()
+    for _ in range(10):
+        pa.call("pa_memcpy", dst.data_ptr(), src.data_ptr(), nbytes, pa.PA_MEMCPY_DEVICE_TO_DEVICE, stream.handle)
+    stream.synchronize()
+    log(f"[bench] copy calibration: 10 x {nbytes} bytes device-to-device")
+
+
 GRAPH_CALLS = 32  # layer-steps per captured graph: one decode step of a 32-layer (Llama-3-8B) model
 
 
@@ -466,13 +511,15 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="budget of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--only-step", action="store_true",
-                    help="time the headline step only (no two-call comparison, no other configurations, no "
-                         "CPU baseline): for profiling")
+                    help="time the headline step only (two pools alternating; no one-pool or two-call comparison, "
+                         "no other configurations, no CPU baseline): for profiling")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 measurements")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time the C3 chunked prefill call only and print its own JSON line: for profiling")
     ap.add_argument("--only-c5", action="store_true",
                     help="time C5 through pa_paged_decode and pa_paged_decode_prefix and print their JSON line")
+    ap.add_argument("--only-c4", action="store_true",
+                    help="time the C4 step (int8 fused append + decode) only and print its JSON line: for profiling")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run 10 plain device-to-device copies of this many MiB through pa_memcpy, the "
                          "reference kernel for scaling hardware byte counters")
@@ -503,6 +550,13 @@ def main():
         flops = float(4 * w3.num_q_heads * w3.head_dim * np.sum(P * L + L * (L + 1) / 2))
         print(json.dumps({"mode": "only-prefill", "workload": "C3 chunked prefill", "us": round(ms * 1e3, 3),
                           "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "steps": args.steps}), flush=True)
+        copy_calibration(args, stream)
+        return
+    if args.only_c4:
+        c4 = run_decode_config(wl.make_c4(), timer, stream, args.steps, args.warmup, True, 4)
+        print(json.dumps({"mode": "only-c4", "workload": "C4 int8 fused append + decode", **c4,
+                          "steps": args.steps}), flush=True)
+        copy_calibration(args, stream)
         return
     if args.only_c5:
         w5 = wl.make_c5()
@@ -521,17 +575,26 @@ def main():
         pa.paged_decode(stream, cfg, out, inp["q"], inp["k_cache"], inp["v_cache"], None, None,
                         inp["tables"], inp["lens"], S, w.max_blocks, w.max_context_len, ws, wsb)
 
-    step_ms = timer(step, args.steps, args.warmup)
+    step_ms, two_pool = run_two_pool(w, inp, timer, stream, cfg, args.steps, args.warmup)
+    log(f"[bench] C2 fused step alternating two cache pools {step_ms * 1e3:.2f} us")
     two_call_ms = float("nan")
     graph_ms = float("nan")
+    one_pool = None
     extra = None
     if not args.only_step:
+        one_ms = timer(step, args.steps, args.warmup)
+        one_gbps = (w.decode_algorithmic_bytes() + append_bytes(w)) / (one_ms * 1e-3) / 1e9
+        one_pool = {"us_per_layer_step": round(one_ms * 1e3, 3), "gbps": round(one_gbps, 1),
+                    "frac_hbm": round(one_gbps / PEAK_HBM_GBPS, 4),
+                    "step": "pa_paged_decode_append repeated over one pool (part of K/V still in the 256 MB "
+                            "last-level cache from the step before)"}
         pos = w.context_lens.astype(np.int64) - 1
         inp["slots"] = tensor(w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16)
         two_call_ms = timer(two_call_step, args.steps, args.warmup)
-        log(f"[bench] C2 fused step {step_ms * 1e3:.2f} us, two-call step {two_call_ms * 1e3:.2f} us")
+        log(f"[bench] C2 fused step over one pool {one_ms * 1e3:.2f} us, two-call step (one pool) "
+            f"{two_call_ms * 1e3:.2f} us")
         graph_ms = time_graph_replay(step, timer, stream, args.steps)
-        log(f"[bench] C2 fused step replayed from a captured graph of {GRAPH_CALLS} steps "
+        log(f"[bench] C2 fused step replayed from a captured graph of {GRAPH_CALLS} steps (one pool) "
             f"{graph_ms * 1e3:.2f} us per step")
         if not args.no_extra:
             extra = {}
@@ -555,14 +618,7 @@ def main():
             log(f"[bench] C2 layer with projections {extra['C2_layer']}")
             torch.cuda.empty_cache()
     torch.cuda.synchronize()
-    if args.copy_calibration_mb > 0:
-        nbytes = args.copy_calibration_mb << 20
-        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
-        for _ in range(10):
-            pa.call("pa_memcpy", dst.data_ptr(), src.data_ptr(), nbytes, pa.PA_MEMCPY_DEVICE_TO_DEVICE, stream.handle)
-        stream.synchronize()
-        log(f"[bench] copy calibration: 10 x {nbytes} bytes device-to-device")
+    copy_calibration(args, stream)
 
     dec_bytes = w.decode_algorithmic_bytes()
     step_bytes = dec_bytes + append_bytes(w)
@@ -589,7 +645,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "C2: Llama-3-8B-shaped single-layer paged decode (append + attention), bf16 KV, "
-                        "fp32 accumulate",
+                        "fp32 accumulate; steps alternate two cache pools (cold HBM)",
             "num_seqs": S, "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
             "head_dim": w.head_dim, "block_size": 16, "context_lens": "log-uniform [128, 4096]",
             "context_tokens": int(w.context_lens.sum()), "num_blocks": w.num_blocks,
@@ -614,6 +670,8 @@ def main():
         "two_call_us_per_layer_step": None if two_call_ms != two_call_ms else round(two_call_ms * 1e3, 3),
         "graph_replay_us_per_layer_step": None if graph_ms != graph_ms else round(graph_ms * 1e3, 3),
         "graph_layer_steps_per_replay": GRAPH_CALLS,
+        "two_pool": two_pool,
+        "one_pool": one_pool,
         "extra": extra,
         "cpu_baseline": cpu,
         "device": {"name": props.name.decode(), "arch": props.arch.decode(), "cus": props.compute_units},
