@@ -249,6 +249,10 @@ class Stream:
     def synchronize(self):
         call("pa_stream_synchronize", self.handle)
 
+    def wait_event(self, event: "Event"):
+        """Work enqueued on this stream from now on starts after `event`'s recorded work."""
+        call("pa_stream_wait_event", self.handle, event.handle)
+
     def destroy(self):
         if self.handle:
             call("pa_stream_destroy", self.handle)
