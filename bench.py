@@ -415,11 +415,18 @@ def run_block_moves(timer, stream, steps, warmup, seed):
             "gather_blocks_gbps": round(moved / (ms_gather * 1e-3) / 1e9, 1)}
 
 
+WEIGHT_ROTATION_BYTES = 320 << 20  # more than the 256 MB last-level cache
+
+
 def run_layer(timer, stream, w, inp, steps, warmup, seed):
     """One whole decode layer of the C2 batch with Llama-3-8B projection weights (hidden 4096,
     bf16): pa_qkv_project_append (x . W_qkv^T, Q out, K/V appended), pa_paged_decode over the
     cache, pa_o_project. Times each call and the three in sequence; the GEMMs are weight-bound, so
-    their rate is weight bytes per second."""
+    their rate is weight bytes per second. Successive calls cycle through copies of each weight that
+    together exceed the last-level cache, as the layers of a model do (each has its own weights),
+    so the weights come from HBM."""
+    import itertools
+
     import torch
 
     hidden, S = 4096, w.num_seqs
@@ -431,10 +438,12 @@ def run_layer(timer, stream, w, inp, steps, warmup, seed):
     x = bf(S, hidden)
     w_qkv = bf((hq + 2 * hkv) * d, hidden)
     w_o = bf(hidden, hq * d)
+    copies = lambda t: itertools.cycle([t] + [t.clone() for _ in range(-(-WEIGHT_ROTATION_BYTES // (t.numel() * 2)) - 1)])
+    wq_cycle, wo_cycle = copies(w_qkv), copies(w_o)
     q = torch.empty((S, hq, d), dtype=torch.bfloat16, device="cuda:0")
     attn = torch.empty((S, hq, d), dtype=torch.float32, device="cuda:0")
     y = torch.empty((S, hidden), dtype=torch.float32, device="cuda:0")
-    qws_b, ows_b = pa.qkv_workspace_size(cfg, S), pa.o_workspace_size(cfg, S)
+    qws_b, ows_b = pa.qkv_workspace_size(cfg, S), pa.o_workspace_size(cfg, hidden, S)
     qws = torch.empty(qws_b, dtype=torch.uint8, device="cuda:0")
     ows = torch.empty(ows_b, dtype=torch.uint8, device="cuda:0")
     dws_b = pa.decode_workspace_size(cfg, S, w.max_context_len)
@@ -443,15 +452,15 @@ def run_layer(timer, stream, w, inp, steps, warmup, seed):
     slots = tensor(w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16)
 
     def qkv():
-        pa.qkv_project_append(stream, cfg, x, w_qkv, hidden, S, slots, q, inp["k_cache"], inp["v_cache"], None, None,
-                              None, None, qws, qws_b)
+        pa.qkv_project_append(stream, cfg, x, next(wq_cycle), hidden, S, slots, q, inp["k_cache"], inp["v_cache"],
+                              None, None, None, None, qws, qws_b)
 
     def dec():
         pa.paged_decode(stream, cfg, attn, q, inp["k_cache"], inp["v_cache"], None, None, inp["tables"], inp["lens"],
                         S, w.max_blocks, w.max_context_len, dws, dws_b)
 
     def oproj():
-        pa.o_project(stream, cfg, attn, w_o, hidden, S, y, ows, ows_b)
+        pa.o_project(stream, cfg, attn, next(wo_cycle), hidden, S, y, ows, ows_b)
 
     def layer():
         qkv(); dec(); oproj()
@@ -460,7 +469,8 @@ def run_layer(timer, stream, w, inp, steps, warmup, seed):
     stream.synchronize()
     t = {k: timer(f, steps, warmup) * 1e3 for k, f in (("qkv", qkv), ("decode", dec), ("o", oproj), ("layer", layer))}
     wq_bytes, wo_bytes = w_qkv.numel() * 2, w_o.numel() * 2
-    return {"hidden": hidden, "qkv_project_append_us": round(t["qkv"], 2),
+    return {"hidden": hidden, "weights": "cycled through copies over 320 MB (HBM, not the last-level cache)",
+            "qkv_project_append_us": round(t["qkv"], 2),
             "qkv_weight_gbps": round(wq_bytes / (t["qkv"] * 1e-6) / 1e9, 1),
             "decode_us": round(t["decode"], 2), "o_project_us": round(t["o"], 2),
             "o_weight_gbps": round(wo_bytes / (t["o"] * 1e-6) / 1e9, 1), "layer_us": round(t["layer"], 2)}
@@ -518,6 +528,8 @@ def main():
                     help="time the C3 chunked prefill call only and print its own JSON line: for profiling")
     ap.add_argument("--only-c5", action="store_true",
                     help="time C5 through pa_paged_decode and pa_paged_decode_prefix and print their JSON line")
+    ap.add_argument("--only-layer", action="store_true",
+                    help="time only the C2 decode layer with its projections (and print that)")
     ap.add_argument("--only-c4", action="store_true",
                     help="time the C4 step (int8 fused append + decode) only and print its JSON line: for profiling")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -564,6 +576,11 @@ def main():
         shared = run_prefix_decode(w5, timer, stream, args.steps, args.warmup, 5)
         print(json.dumps({"mode": "only-c5", "workload": "C5 decode", "pa_paged_decode": plain,
                           "pa_paged_decode_prefix": shared, "steps": args.steps}), flush=True)
+        return
+    if args.only_layer:
+        lay = run_layer(timer, stream, w, inp, args.steps, args.warmup, 5)
+        print(json.dumps({"mode": "only-layer", "workload": "C2 decode layer with projections", **lay,
+                          "steps": args.steps}), flush=True)
         return
     cfg = config_of(w, args.partition_size)
     S = w.num_seqs

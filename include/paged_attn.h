@@ -378,11 +378,16 @@ pa_status pa_write_block_f32(pa_stream* stream, const pa_config* cfg, void* k_ca
  *      _queryProj/_keyProj/_valueProj.Forward + UpdateKVCache and _outputProj.Forward,
  *      Layers/PagedAttentionLayer.cs:112-142; Linear.Forward y = x W^T without bias,
  *      Modules/Linear.cs:81-110). bf16 weights and activations (cfg->q_dtype must be BF16), fp32
- *      accumulation; the GEMMs run on rocBLAS. The first call on a device creates its rocBLAS
- *      handle, so make one call before capturing these into a graph. ---- */
+ *      accumulation. Batches of at most 64 tokens (decode) run on a weight-streaming MFMA kernel
+ *      with the k range split over workgroups (partials added in a fixed order, so results are
+ *      deterministic); larger batches, and operands not 16-byte aligned or with the reduced
+ *      dimension not a multiple of 128, run on rocBLAS. The first rocBLAS call on a device creates
+ *      its handle, so make one call of that shape before capturing these into a graph. ---- */
 
-/* Bytes of workspace pa_qkv_project_append needs for n_tok tokens: the fp32 GEMM output
- * [n_tok][(num_q_heads + 2 num_kv_heads) head_dim]. */
+/* Bytes of workspace pa_qkv_project_append needs for n_tok tokens: for n_tok <= 64, the split
+ * partials [splits][n_tok][(num_q_heads + 2 num_kv_heads) head_dim] fp32 (splits <= 8); above,
+ * the fp32 GEMM output [n_tok][(num_q_heads + 2 num_kv_heads) head_dim]. Either way the GEMM
+ * output y sits at the start of the workspace after the call. */
 pa_status pa_qkv_workspace_size(const pa_config* cfg, int32_t n_tok, size_t* bytes);
 /* x [n_tok][hidden] bf16; w_qkv [(Hq + 2 Hkv) * head_dim][hidden] bf16, the rows of Wq, then Wk,
  * then Wv. y = x w_qkv^T (fp32); q_out [n_tok][Hq][head_dim] (bf16) = y's Q columns truncated; the
@@ -392,8 +397,10 @@ pa_status pa_qkv_project_append(pa_stream* stream, const pa_config* cfg, const v
                                 int32_t hidden, int32_t n_tok, const int64_t* slot_mapping, void* q_out,
                                 void* k_cache, void* v_cache, float* k_scale, float* v_scale,
                                 float* k_absmax, float* v_absmax, void* workspace, size_t workspace_bytes);
-/* Bytes of workspace pa_o_project needs for n_tok tokens (a bf16 copy of the attention output). */
-pa_status pa_o_workspace_size(const pa_config* cfg, int32_t n_tok, size_t* bytes);
+/* Bytes of workspace pa_o_project needs for n_tok tokens and `hidden` output columns: for
+ * n_tok <= 64 the larger of the split partials [splits - 1][n_tok][hidden] fp32 and a bf16 copy
+ * of the attention output; above, the bf16 copy. */
+pa_status pa_o_workspace_size(const pa_config* cfg, int32_t hidden, int32_t n_tok, size_t* bytes);
 /* attn [n_tok][Hq][head_dim] fp32 (the decode / prefill output), truncated to bf16;
  * w_o [hidden][Hq * head_dim] bf16; y [n_tok][hidden] fp32 = attn_bf16 w_o^T. */
 pa_status pa_o_project(pa_stream* stream, const pa_config* cfg, const float* attn, const void* w_o,

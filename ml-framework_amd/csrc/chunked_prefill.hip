@@ -103,33 +103,6 @@ template <int D, int ELT> struct PrefillTile {
     __device__ static constexpr int vsrc(int p, int b) { return VRC == 2 ? p ^ b : p; }
 };
 
-// 16 bytes per lane from a buffer into LDS: lane l's bytes land at LDS address lds + 16 l
-// (buffer_load_dwordx4 with the LDS bit; M0 holds the LDS address, and one wait state must
-// separate the M0 write from the load; M0 is restored afterwards). A zero-sized descriptor
-// writes zeros. Written as inline asm so that the compiler, which does not see these LDS
-// writes, adds no wait on them before its own LDS reads: the kernel orders them itself (vmcnt
-// wait + barrier per step). The LDS address is an operand and the asm clobbers memory, so the
-// compiler treats the array as written by it.
-using u32x4_t = uint32_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void lds_load16(u32x4_t rsrc, uint32_t voffset, uint32_t lds) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %1, 0 offen lds\n\ts_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(rsrc), "v"(voffset), "s"(lds)
-        : "memory");
-}
-__device__ __forceinline__ u32x4_t buffer_rsrc_words(const void* base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    return u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
-                   static_cast<uint32_t>(kBufferFlags)};
-}
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    using lds_char = const __attribute__((address_space(3))) char;
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)p));  // generic -> LDS offset
-}
-
 // Work units are (16-query tile, query head) pairs of one KV head. A workgroup takes QT =
 // max(1, kPrefillUnits / G) consecutive query tiles, i.e. QT * G units, kPrefillUnits at a time:
 // wave w computes units 2w and 2w + 1 of the round on the same K/V operands (each LDS operand

@@ -157,7 +157,7 @@ _SIGNATURES = {
     "pa_write_block_f32": [_P, _CFG, _P, _P, _P, _P, _P, _P, _I32, _I32, _P, _P],
     "pa_qkv_workspace_size": [_CFG, _I32, ctypes.POINTER(_SZ)],
     "pa_qkv_project_append": [_P, _CFG, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ],
-    "pa_o_workspace_size": [_CFG, _I32, ctypes.POINTER(_SZ)],
+    "pa_o_workspace_size": [_CFG, _I32, _I32, ctypes.POINTER(_SZ)],
     "pa_o_project": [_P, _CFG, _P, _P, _I32, _I32, _P, _P, _SZ],
 }
 
@@ -462,9 +462,9 @@ def qkv_project_append(stream, cfg: PaConfig, x, w_qkv, hidden, n_tok, slot_mapp
          _ptr(k_absmax), _ptr(v_absmax), _ptr(workspace), workspace_bytes)
 
 
-def o_workspace_size(cfg: PaConfig, n_tok: int) -> int:
+def o_workspace_size(cfg: PaConfig, hidden: int, n_tok: int) -> int:
     n = ctypes.c_size_t()
-    call("pa_o_workspace_size", ctypes.byref(cfg), n_tok, ctypes.byref(n))
+    call("pa_o_workspace_size", ctypes.byref(cfg), hidden, n_tok, ctypes.byref(n))
     return n.value
 
 
