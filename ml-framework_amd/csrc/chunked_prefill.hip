@@ -20,9 +20,11 @@
 // S^T[32 keys][16 queries] = K . Q^T on two v_mfma_f32_16x16x32_bf16 per 32 dims, whose rows are
 // permuted so every lane ends up with 8 consecutive keys of one block; online softmax per query
 // in fp32 (log2 domain, rescale only past a 2^12 margin, mask only on the pairs at the causal
-// edge); O[16 queries][D] += P . V on v_mfma_f32_16x16x32_bf16 with P split into bf16 high and
-// low parts and the lane's 8 keys as the k range, the V operand one 16-byte LDS read; the row
-// sums of P from the same MFMA against ones.
+// edge); O[16 queries][D] += P . V with the lane's 8 keys as the k range and the V operand one
+// 16-byte LDS read: for bf16 caches on v_mfma_f32_16x16x32_f16 with one fp16 P (V converted to
+// fp16 in LDS by the wave that loaded it), for int8 caches on v_mfma_f32_16x16x32_bf16 with P
+// split into bf16 high and low parts; the row sums of P from the same MFMA against ones. Without
+// the low parts the D = 128 kernel fits three workgroups per CU.
 #include <string>
 
 #include "decode_common.h"
@@ -108,7 +110,7 @@ template <int D, int ELT> struct PrefillTile {
 // wave w computes units 2w and 2w + 1 of the round on the same K/V operands (each LDS operand
 // read feeds both).
 template <int D, int KV, bool QF32>
-__global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) void chunked_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 : 3)) void chunked_prefill_kernel(const PrefillArgs a) {
     using Raw = MfmaRaw<KV>;
     constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
     // QK operand row of this lane (see compute) and the keys it holds after QK (for P and V)
     const int krow0 = (n & 3) + 8 * (n >> 3), kblk = (n >> 2) & 1;
     const int pblk = q4 & 1, ptok = 8 * (q4 >> 1);
-    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+    const f16x8_t ones16 = __builtin_bit_cast(f16x8_t, make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u));
 
     const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
     const char* kc = static_cast<const char*>(a.k_cache);
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
         seg_off[k] = 16 * ((t & 1) ? TL::vsrc(pos, b) : TL::ksrc(pos));
     }
     // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS.
-    constexpr int KCH = 1024;
+    constexpr int KCH = D > 64 ? 512 : 1024;  // 3 workgroups per CU at D = 128 fit the LDS with 512
     __shared__ int s_ids[KCH];
     __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1];
     const uint32_t tile_lds = lds_address(s_tile);
@@ -338,9 +340,37 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                         for (int i = 0; i < 4; i++) acc[k][t][i] *= ar[i];
                 }
             }
-            // P of both units (high and low bf16 parts) first, then each V operand is read from LDS
-            // right before the four MFMAs that use it: holding all NT V operands across the two
-            // units' PV products pushed the kernel past 256 VGPRs into scratch spills, whose
+            if constexpr (ELT == 2) {
+                // bf16 caches: one fp16 P per probability (rounded to nearest, relative error <=
+                // 2^-11; P <= 2^12 by the rescale margin) against V in fp16 (converted in LDS when
+                // its tiles land, exact for 2^-14 <= |v| <= 65504): one PV MFMA per unit and tile
+                // and one row-sum MFMA. The P of both units first, then each V operand is read
+                // right before the MFMAs that use it.
+                f16x8_t pf[2];
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const half2_t h = {static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(v[k][2 * e], c2, -m_run[k]))),
+                                           static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(v[k][2 * e + 1], c2, -m_run[k])))};
+                        w[e] = __builtin_bit_cast(uint32_t, h);
+                    }
+                    pf[k] = __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+                }
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const int d = 16 * t + n;
+                    const f16x8_t vop = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
+#pragma unroll
+                    for (int k = 0; k < 2; k++) acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], vop, acc[k][t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 2; k++) acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], ones16, acc_l[k], 0, 0, 0);
+            } else {
+            // int8 caches: P of both units (high and low bf16 parts) first, then each V operand is
+            // read from LDS right before the four MFMAs that use it: holding all NT V operands across
+            // the two units' PV products pushed the kernel past 256 VGPRs into scratch spills, whose
             // reloads inside the loop wait for every load in flight.
             bf16x8_t phi[2], plo[2];
 #pragma unroll
@@ -382,12 +412,6 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
                     acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[k], vop, acc[k][t], 0, 0, 0);
                 }
             }
-            if constexpr (KV != PA_DTYPE_INT8) {
-#pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[k], ones, acc_l[k], 0, 0, 0);
-                    acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[k], ones, acc_l[k], 0, 0, 0);
-                }
             }
         };
 
@@ -425,7 +449,31 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 ? 2 : 3)) vo
             int slot = 0, load_slot = 2;  // slots of pair jp and of pair jp + 2
             for (int jp = 0; jp < npair; jp++) {
                 static_assert(NSEG <= 15, "vmcnt immediate");
-                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(NSEG) : "memory");
+                if constexpr (ELT == 2) {
+                    // This wave's segments of pair jp have landed: it turns its V chunks into fp16
+                    // in place (same positions) before meeting the others, so the barrier publishes
+                    // whole fp16 V tiles. Round toward zero: exact for every bf16 value fp16
+                    // represents, larger magnitudes saturate at 65504.
+                    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NSEG) : "memory");
+#pragma unroll
+                    for (int k = 0; k < NSEG; k++) {
+                        const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT;
+                        if (t & 1) {
+                            uint4* c = s_tile + (TL::base(slot, t >> 1) + TL::K_CHUNKS + (sg % TL::SPT) * 64 + lane);
+                            const uint4 x = *c;
+                            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+                            uint32_t o[4];
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
+                                                                                                 __uint_as_float(w[e] & 0xffff0000u)));
+                            *c = make_uint4(o[0], o[1], o[2], o[3]);
+                        }
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+                } else {
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(NSEG) : "memory");
+                }
                 issue(2 * (jp + 2), nkc, load_slot);
                 const int lb = c0 + 2 * jp;
                 compute((lb + 2) * 16 > kend_lo, kend, slot, lb, 2 * jp);
