@@ -20,11 +20,11 @@
 // S^T[32 keys][16 queries] = K . Q^T on two v_mfma_f32_16x16x32_bf16 per 32 dims, whose rows are
 // permuted so every lane ends up with 8 consecutive keys of one block; online softmax per query
 // in fp32 (log2 domain, rescale only past a 2^12 margin, mask only on the pairs at the causal
-// edge); O[16 queries][D] += P . V with the lane's 8 keys as the k range and the V operand one
-// 16-byte LDS read: for bf16 caches on v_mfma_f32_16x16x32_f16 with one fp16 P (V converted to
-// fp16 in LDS by the wave that loaded it), for int8 caches on v_mfma_f32_16x16x32_bf16 with P
-// split into bf16 high and low parts; the row sums of P from the same MFMA against ones. Without
-// the low parts the D = 128 kernel fits three workgroups per CU.
+// edge); O[16 queries][D] += P . V on v_mfma_f32_16x16x32_f16 with one fp16 P and the lane's 8
+// keys as the k range, the V operand one 16-byte LDS read (bf16 tiles converted to fp16 in LDS by
+// the wave that loaded them; int8 codes converted in registers); the row sums of P from the same
+// MFMA against ones. With one P operand instead of bf16 high and low parts the D = 128 kernel fits
+// three workgroups per CU.
 #include <string>
 
 #include "decode_common.h"
@@ -340,39 +340,13 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                         for (int i = 0; i < 4; i++) acc[k][t][i] *= ar[i];
                 }
             }
-            if constexpr (ELT == 2) {
-                // bf16 caches: one fp16 P per probability (rounded to nearest, relative error <=
-                // 2^-11; P <= 2^12 by the rescale margin) against V in fp16 (converted in LDS when
-                // its tiles land, exact for 2^-14 <= |v| <= 65504): one PV MFMA per unit and tile
-                // and one row-sum MFMA. The P of both units first, then each V operand is read
-                // right before the MFMAs that use it.
-                f16x8_t pf[2];
-#pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    uint32_t w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const half2_t h = {static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(v[k][2 * e], c2, -m_run[k]))),
-                                           static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(v[k][2 * e + 1], c2, -m_run[k])))};
-                        w[e] = __builtin_bit_cast(uint32_t, h);
-                    }
-                    pf[k] = __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
-                }
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const int d = 16 * t + n;
-                    const f16x8_t vop = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
-#pragma unroll
-                    for (int k = 0; k < 2; k++) acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], vop, acc[k][t], 0, 0, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < 2; k++) acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], ones16, acc_l[k], 0, 0, 0);
-            } else {
-            // int8 caches: P of both units (high and low bf16 parts) first, then each V operand is
-            // read from LDS right before the four MFMAs that use it: holding all NT V operands across
-            // the two units' PV products pushed the kernel past 256 VGPRs into scratch spills, whose
-            // reloads inside the loop wait for every load in flight.
-            bf16x8_t phi[2], plo[2];
+            // One fp16 P per probability (rounded to nearest, relative error <= 2^-11; P <= 2^12 by
+            // the rescale margin; int8: P times the block's V scale) against V in fp16: bf16 caches'
+            // tiles were converted in LDS when they landed (exact for 2^-14 <= |v| <= 65504), int8
+            // codes are converted here (exact). One PV MFMA per unit and 16-dim tile; bf16 row sums
+            // from one more MFMA against ones, int8 row sums in l_run (before the V scale). The P
+            // of both units first, then each V operand is read right before the MFMAs that use it.
+            f16x8_t pf[2];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 float p[8];
@@ -381,37 +355,44 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                     if constexpr (KV == PA_DTYPE_INT8) p[e] = __builtin_amdgcn_exp2f(v[k][e] - m_run[k]);
                     else p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[k][e], c2, -m_run[k]));
                 }
-                if constexpr (KV == PA_DTYPE_INT8) {  // the row sums take P before the block's V scale
+                if constexpr (KV == PA_DTYPE_INT8) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) l_run[k] += p[e];
                     const float vs = s_vsc[jl + pblk];
 #pragma unroll
                     for (int e = 0; e < 8; e++) p[e] *= vs;
                 }
-                uint32_t hi[4], lo[4];
+                uint32_t w[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float a0 = p[2 * e], a1 = p[2 * e + 1];
-                    const float h0 = __uint_as_float(__float_as_uint(a0) & 0xffff0000u);
-                    const float h1 = __uint_as_float(__float_as_uint(a1) & 0xffff0000u);
-                    hi[e] = pack_bf16_trunc(a0, a1);
-                    lo[e] = pack_bf16_trunc(a0 - h0, a1 - h1);
+                    const half2_t h = {static_cast<_Float16>(p[2 * e]), static_cast<_Float16>(p[2 * e + 1])};
+                    w[e] = __builtin_bit_cast(uint32_t, h);
                 }
-                phi[k] = __builtin_bit_cast(bf16x8_t, make_uint4(hi[0], hi[1], hi[2], hi[3]));
-                plo[k] = __builtin_bit_cast(bf16x8_t, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                pf[k] = __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
             }
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const int d = 16 * t + n;
-                bf16x8_t vop;
-                if constexpr (ELT == 2) vop = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
-                else vop = k_operand(*reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0, pblk) * 16 + (q4 >> 1) * 8));
+                f16x8_t vop;
+                if constexpr (ELT == 2) {
+                    vop = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
+                } else {
+                    const uint2 c = *reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0, pblk) * 16 + (q4 >> 1) * 8);
+                    uint32_t o[4];
 #pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(phi[k], vop, acc[k][t], 0, 0, 0);
-                    acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(plo[k], vop, acc[k][t], 0, 0, 0);
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t x = e < 2 ? c.x : c.y;
+                        o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(pa::i8_at(x, 2 * (e & 1)),
+                                                                                         pa::i8_at(x, 2 * (e & 1) + 1)));
+                    }
+                    vop = __builtin_bit_cast(f16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
                 }
+#pragma unroll
+                for (int k = 0; k < 2; k++) acc[k][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], vop, acc[k][t], 0, 0, 0);
             }
+            if constexpr (KV != PA_DTYPE_INT8) {
+#pragma unroll
+                for (int k = 0; k < 2; k++) acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], ones16, acc_l[k], 0, 0, 0);
             }
         };
 
