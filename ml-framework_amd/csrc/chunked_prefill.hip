@@ -137,6 +137,9 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Which tile each of the wave's load segments belongs to follows from the wave index; with
+    // the range known, the compiler resolves it at compile time where the tile size allows.
+    __builtin_assume(wave >= 0 && wave < kPrefillWaves);
     const int q4 = lane >> 4, n = lane & 15;
     const int G = a.group, Hkv = a.num_kv_heads, Hq = Hkv * G;
     const int QT = a.qtiles_per_wg;
@@ -284,6 +287,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                         kop[sl] = k_operand(*reinterpret_cast<const KR*>(tk + TL::kpos(r, cc) * 16 + (q4 & 1) * 8));
                     }
                 }
+                __builtin_amdgcn_s_setprio(2);
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
                     f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -295,6 +299,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
 #pragma unroll
                     for (int i = 0; i < 4; i++) v[k][4 * h + i] = sacc[i];
                 }
+                __builtin_amdgcn_s_setprio(0);
             }
             if constexpr (KV == PA_DTYPE_INT8) {
                 const float mult = c2 * s_ksc[jl + pblk];  // 0 for an invalid block
@@ -370,6 +375,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 }
                 pf[k] = __builtin_bit_cast(f16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
             }
+            __builtin_amdgcn_s_setprio(2);
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const int d = 16 * t + n;
@@ -394,6 +400,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
 #pragma unroll
                 for (int k = 0; k < 2; k++) acc_l[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[k], ones16, acc_l[k], 0, 0, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
         };
 
         // Stream, a pair of blocks per step: pair j (blocks 2j, 2j + 1 of the chunk) was loaded
