@@ -183,15 +183,31 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
     // Loads of the pair of blocks jl, jl + 1 (of the current chunk of the table) into slot `slot`.
     // A block past the chunk or with an invalid id gets a zero-sized descriptor and reads as zeros,
     // so every wave issues the same NSEG loads per pair and one vmcnt value covers them all.
+    // Block ids are read from a register that holds 64 of them (lane l: id of block 64w + l of the
+    // chunk), refilled from LDS when the stream enters the next 64 blocks, so an issue does not
+    // wait for an LDS read; each block's tile offset is computed once for its K and V descriptors.
+    int ids_win = -1, ids_v = -1;
+    auto block_id = [&](int j, int nkc) -> int {  // j wave-uniform
+        if (j >= nkc) return -1;
+        if ((j >> 6) != ids_win) {
+            ids_win = j >> 6;
+            const int jj = (ids_win << 6) + lane;
+            ids_v = jj < nkc ? s_ids[jj] : -1;
+        }
+        return __builtin_amdgcn_readlane(ids_v, j & 63);
+    };
     auto issue = [&](int jl, int nkc, int slot) {
-        const int id0 = __builtin_amdgcn_readfirstlane(jl < nkc ? s_ids[jl] : -1);
-        const int id1 = __builtin_amdgcn_readfirstlane(jl + 1 < nkc ? s_ids[jl + 1] : -1);
+        int id[2];
+        int64_t tile[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            id[b] = block_id(jl + b, nkc);
+            tile[b] = (static_cast<int64_t>(id[b] >= 0 ? id[b] : 0) * Hkv + kvh) * TILE * ELT;
+        }
 #pragma unroll
         for (int k = 0; k < NSEG; k++) {
             const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT, b = t >> 1;
-            const int bid = b ? id1 : id0;
-            const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
-            const u32x4_t rsrc = buffer_rsrc_words(((t & 1) ? vc : kc) + tile, bid >= 0 ? TILE * ELT : 0);
+            const u32x4_t rsrc = buffer_rsrc_words(((t & 1) ? vc : kc) + tile[b], id[b] >= 0 ? TILE * ELT : 0);
             const int lpos = TL::base(slot, b) + ((t & 1) ? TL::K_CHUNKS : 0) + (sg % TL::SPT) * 64;
             lds_load16(rsrc, seg_off[k], tile_lds + 16 * lpos);
         }
@@ -432,6 +448,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 }
             }
             __syncthreads();
+            ids_win = -1;
             issue(0, nkc, 0);
             issue(2, nkc, 1);
             int slot = 0, load_slot = 2;  // slots of pair jp and of pair jp + 2
