@@ -110,7 +110,8 @@ def test_append_plain_bit_exact(stream, kv_dtype, q_dtype, D):
     np.testing.assert_array_equal(to_np(gv, cdt), vc)
 
 
-@pytest.mark.parametrize("kv_dtype,q_dtype,D", [(1, 1, 128), (0, 0, 64), (1, 0, 256), (0, 1, 128)])
+@pytest.mark.parametrize("kv_dtype,q_dtype,D", [(1, 1, 128), (0, 0, 64), (1, 0, 256), (0, 1, 128), (1, 1, 32),
+                                                (0, 0, 32)])
 def test_append_plain_whole_blocks_bit_exact(stream, kv_dtype, q_dtype, D):
     """Runs of 16 consecutive slots that fill a block take the kernel's whole-tile V path; the
     rest (partial runs, a run crossing a block boundary, one broken by an invalid slot or out of
@@ -142,6 +143,79 @@ def test_append_plain_whole_blocks_bit_exact(stream, kv_dtype, q_dtype, D):
     orc.kv_append(cfg, src_k, src_v, slots, kc, vc)
     pa.kv_append(stream, cfg, to_gpu(src_k), to_gpu(src_v), to_gpu(slots), n, gk, gv)
     _sync()
+    np.testing.assert_array_equal(to_np(gk, cdt), kc)
+    np.testing.assert_array_equal(to_np(gv, cdt), vc)
+
+
+@pytest.mark.parametrize("kv_dtype,q_dtype,D", [(1, 1, 128), (0, 1, 64), (1, 0, 256)])
+def test_append_prefill_chunks_bit_exact(stream, kv_dtype, q_dtype, D):
+    """Chunks of several sequences in one call, as a chunked-prefill step appends them: each chunk
+    starts at an arbitrary position of its sequence (a partly filled first block), fills whole
+    blocks whose 16 tokens straddle the call's 16-token groups, and may end mid-block."""
+    rng = np.random.default_rng(90 + D + kv_dtype)
+    hkv, nb = 2, 64
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=kv_dtype,
+                         q_dtype=q_dtype, num_blocks=nb)
+    perm = rng.permutation(nb)
+    prefix, chunk = [37, 0, 15, 100], [50, 33, 64, 45]
+    slots, used = [], 0
+    for p, c in zip(prefix, chunk):
+        nblk = (p + c + 15) // 16
+        tab = perm[used:used + nblk]
+        used += nblk
+        pos = p + np.arange(c)
+        slots.append(tab[pos // 16].astype(np.int64) * 16 + pos % 16)
+    slots = np.concatenate(slots)
+    n = len(slots)
+    src_k = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    src_v = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    if q_dtype == 1:
+        src_k, src_v = orc.bf16_from_f32(src_k), orc.bf16_from_f32(src_v)
+    cdt = np.uint16 if kv_dtype == 1 else np.float32
+    init = rng.standard_normal((nb, hkv, 16, D), dtype=np.float32)
+    kc = orc.bf16_from_f32(init) if kv_dtype == 1 else init.copy()
+    vc = kc.copy()
+    gk, gv = to_gpu(kc), to_gpu(vc)
+    orc.kv_append(cfg, src_k, src_v, slots, kc, vc)
+    pa.kv_append(stream, cfg, to_gpu(src_k), to_gpu(src_v), to_gpu(slots), n, gk, gv)
+    _sync()
+    np.testing.assert_array_equal(to_np(gk, cdt), kc)
+    np.testing.assert_array_equal(to_np(gv, cdt), vc)
+
+
+@pytest.mark.parametrize("kv_dtype,q_dtype", [(1, 1), (0, 0)])
+def test_append_plain_unaligned_activations(stream, kv_dtype, q_dtype):
+    """New K/V starting one element past a 16-byte boundary take the element-wise kernel; its
+    bytes equal the oracle's too (whole blocks and partial ones)."""
+    import torch
+
+    rng = np.random.default_rng(95 + kv_dtype)
+    nb, hkv, D = 8, 2, 64
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=kv_dtype,
+                         q_dtype=q_dtype, num_blocks=nb)
+    slots = np.concatenate([np.arange(16) + 16 * 5, np.arange(3, 12) + 16 * 2]).astype(np.int64)
+    n = len(slots)
+    src_k = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    src_v = rng.standard_normal((n, hkv, D), dtype=np.float32)
+    if q_dtype == 1:
+        src_k, src_v = orc.bf16_from_f32(src_k), orc.bf16_from_f32(src_v)
+    cdt = np.uint16 if kv_dtype == 1 else np.float32
+    init = rng.standard_normal((nb, hkv, 16, D), dtype=np.float32)
+    kc = orc.bf16_from_f32(init) if kv_dtype == 1 else init.copy()
+    vc = kc.copy()
+    gk, gv = to_gpu(kc), to_gpu(vc)
+
+    def shifted(a):  # the same values one element into a fresh buffer
+        buf = to_gpu(np.concatenate([np.zeros(1, a.dtype), a.reshape(-1)]))
+        view = buf[1:].view(a.shape)
+        assert view.data_ptr() % 16 != 0
+        return buf, view
+
+    (_, vk), (_, vv) = shifted(src_k), shifted(src_v)
+    orc.kv_append(cfg, src_k, src_v, slots, kc, vc)
+    pa.kv_append(stream, cfg, vk, vv, to_gpu(slots), n, gk, gv)
+    _sync()
+    torch.cuda.synchronize()
     np.testing.assert_array_equal(to_np(gk, cdt), kc)
     np.testing.assert_array_equal(to_np(gv, cdt), vc)
 
