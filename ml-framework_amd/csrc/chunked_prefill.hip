@@ -267,6 +267,8 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         // compiler does not count the slot loads, so it cannot tell them apart there).
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         float m_run[2] = {-INFINITY, -INFINITY};  // log2 units, query n
+        float m_thr[2] = {-INFINITY, -INFINITY};  // scores (as computed, before the log2 scale) above
+                                                  // this may raise m_run past its rescale margin
         float l_run[2] = {0.0f, 0.0f};            // int8: sum of P for query n over this lane's keys
         f32x4_t acc_l[2], acc[2][NT];             // bf16: row sums of P; outputs (queries 4q4 + i)
 #pragma unroll
@@ -276,6 +278,28 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
             for (int t = 0; t < NT; t++) acc[k][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
 
+        // bf16 caches: this wave's V segments of the pair in `slot` (landed: the caller waited for
+        // them) become fp16 in place, same positions. Round toward zero: exact for every bf16 value
+        // fp16 represents, larger magnitudes saturate at 65504. The barrier before the pair is
+        // computed publishes the whole fp16 V tiles.
+        auto convert_v = [&](int slot) {
+#pragma unroll
+            for (int k = 0; k < NSEG; k++) {
+                const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT;
+                if (t & 1) {
+                    uint4* c = s_tile + (TL::base(slot, t >> 1) + TL::K_CHUNKS + (sg % TL::SPT) * 64 + lane);
+                    const uint4 x = *c;
+                    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
+                                                                                         __uint_as_float(w[e] & 0xffff0000u)));
+                    *c = make_uint4(o[0], o[1], o[2], o[3]);
+                }
+            }
+        };
+
         // One pair of blocks (keys lb*16 .. lb*16 + 31), lanes (q4, n): the two QK MFMAs h = 0, 1 take
         // as row r key 8 (r >> 3) + 4h + (r & 3) of block (r >> 2) & 1, so lane (q4, n) receives, for
         // query n, scores e = 4h + i of keys ptok + e of block pblk: 8 consecutive keys of one block.
@@ -284,7 +308,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         // third MFMA against ones, in the accumulators' own layout. Scores are kept in log2 units
         // (scale * log2(e) folded in); pairs with every key below every query's causal limit skip
         // the mask. Both units use the same K and V operands.
-        auto compute = [&](bool masked, int kend, int slot, int lb, int jl) {
+        auto compute = [&](bool masked, int kend, int slot, int next_slot, int lb, int jl) {
             const char* tk = reinterpret_cast<const char*>(s_tile + TL::base(slot, kblk));
             const char* tv = reinterpret_cast<const char*>(s_tile + TL::base(slot, pblk));
             // QK per half h (its 16-row K operands are then dead), V operands after QK
@@ -317,6 +341,12 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 }
                 __builtin_amdgcn_s_setprio(0);
             }
+            if constexpr (ELT == 2) {
+                // While the QK MFMAs run: the next pair's V (its loads, older than the NSEG just
+                // issued, have landed) turns into fp16 for the barrier before that pair.
+                asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NSEG) : "memory");
+                convert_v(next_slot);
+            }
             if constexpr (KV == PA_DTYPE_INT8) {
                 const float mult = c2 * s_ksc[jl + pblk];  // 0 for an invalid block
 #pragma unroll
@@ -333,22 +363,26 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                     for (int e = 0; e < 8; e++) v[k][e] = e < lim ? v[k][e] : -INFINITY;
                 }
             }
-            float bm[2];
-            bool grow[2];
+            // The lane's own maximum against the row's threshold decides whether the row maxima
+            // are needed at all: a row can only grow if one of its lanes holds a score above it.
+            float bl[2];
+            bool over = false;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
-                const float bl = fmaxf(fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])),
-                                       fmaxf(fmaxf(v[k][4], v[k][5]), fmaxf(v[k][6], v[k][7])));
-                bm[k] = rows_max(bl);
-                if constexpr (KV != PA_DTYPE_INT8) bm[k] *= c2;
-                grow[k] = bm[k] > m_run[k] + kPrefillRescaleLog2;
+                bl[k] = fmaxf(fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])),
+                              fmaxf(fmaxf(v[k][4], v[k][5]), fmaxf(v[k][6], v[k][7])));
+                over = over || bl[k] > m_thr[k];
             }
-            if (__any(grow[0] || grow[1])) {
+            if (__any(over)) {
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
-                    const float m_new = grow[k] ? bm[k] : m_run[k];
+                    float bm = rows_max(bl[k]);
+                    if constexpr (KV != PA_DTYPE_INT8) bm *= c2;
+                    const bool grow = bm > m_run[k] + kPrefillRescaleLog2;
+                    const float m_new = grow ? bm : m_run[k];
                     const float alpha = __builtin_amdgcn_exp2f(m_run[k] - m_new);  // 0 on the first update
                     m_run[k] = m_new;
+                    m_thr[k] = KV != PA_DTYPE_INT8 ? (m_new + kPrefillRescaleLog2) / c2 : m_new + kPrefillRescaleLog2;
                     l_run[k] *= alpha;
                     float ar[4];
 #pragma unroll
@@ -420,11 +454,13 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         };
 
         // Stream, a pair of blocks per step: pair j (blocks 2j, 2j + 1 of the chunk) was loaded
-        // into slot j % 3 two steps earlier. Step j waits until this wave's loads of pair j are
-        // done (at most pair j + 1's NSEG loads outstanding; loads complete in order), ends its
-        // LDS reads, and meets the other waves at a barrier; then it loads pair j + 2 into slot
-        // (j + 2) % 3, whose last reader, compute(j - 1), every wave has finished, and computes
-        // pair j. Loads past the chunk's end write zeros into slots nobody reads.
+        // into slot j % 3 two steps earlier. Every wave has waited for its own loads of pair j
+        // (at most pair j + 1's NSEG loads outstanding; loads complete in order): bf16 caches
+        // inside compute(j - 1), after its QK MFMAs, where it also converts its V segments of pair
+        // j to fp16 (pair 0 before the loop); int8 caches at the top of step j. Step j ends the
+        // wave's LDS accesses and meets the other waves at a barrier; then it loads pair j + 2
+        // into slot (j + 2) % 3, whose last reader, compute(j - 1), every wave has finished, and
+        // computes pair j. Loads past the chunk's end write zeros into slots nobody reads.
         for (int c0 = 0; c0 < nkb; c0 += KCH) {
             const int nkc = min(KCH, nkb - c0);
             const int npair = (nkc + 1) / 2;
@@ -451,37 +487,22 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
             ids_win = -1;
             issue(0, nkc, 0);
             issue(2, nkc, 1);
+            if constexpr (ELT == 2) {
+                asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NSEG) : "memory");  // pair 0's segments landed
+                convert_v(0);
+            }
             int slot = 0, load_slot = 2;  // slots of pair jp and of pair jp + 2
             for (int jp = 0; jp < npair; jp++) {
                 static_assert(NSEG <= 15, "vmcnt immediate");
                 if constexpr (ELT == 2) {
-                    // This wave's segments of pair jp have landed: it turns its V chunks into fp16
-                    // in place (same positions) before meeting the others, so the barrier publishes
-                    // whole fp16 V tiles. Round toward zero: exact for every bf16 value fp16
-                    // represents, larger magnitudes saturate at 65504.
-                    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NSEG) : "memory");
-#pragma unroll
-                    for (int k = 0; k < NSEG; k++) {
-                        const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT;
-                        if (t & 1) {
-                            uint4* c = s_tile + (TL::base(slot, t >> 1) + TL::K_CHUNKS + (sg % TL::SPT) * 64 + lane);
-                            const uint4 x = *c;
-                            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-                            uint32_t o[4];
-#pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
-                                                                                                 __uint_as_float(w[e] & 0xffff0000u)));
-                            *c = make_uint4(o[0], o[1], o[2], o[3]);
-                        }
-                    }
+                    // every wave's V segments of pair jp are fp16 (converted during compute(jp - 1))
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
                 } else {
                     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(NSEG) : "memory");
                 }
                 issue(2 * (jp + 2), nkc, load_slot);
                 const int lb = c0 + 2 * jp;
-                compute((lb + 2) * 16 > kend_lo, kend, slot, lb, 2 * jp);
+                compute((lb + 2) * 16 > kend_lo, kend, slot, slot == NSLOT - 1 ? 0 : slot + 1, lb, 2 * jp);
                 slot = slot == NSLOT - 1 ? 0 : slot + 1;
                 load_slot = load_slot == NSLOT - 1 ? 0 : load_slot + 1;
             }
