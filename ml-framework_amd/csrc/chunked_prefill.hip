@@ -53,6 +53,57 @@ struct PrefillArgs {
     int32_t num_groups;     // num_seqs * num_kv_heads
 };
 
+// LDS-direct loads of a wave's run of HS segments of one block's K tile (LDS base m0k) and of its
+// V tile (m0v), 16 bytes a lane: segment j of a run at immediate offset 1024 j, which advances
+// both the memory and the LDS address; off[2j] / off[2j + 1] are the lane's register offsets of
+// K / V segment j. M0 is saved and restored once around all of them.
+template <int HS>
+__device__ __forceinline__ void lds_load_runs(u32x4_t rk, u32x4_t rv, const uint32_t* off, uint32_t m0k,
+                                              uint32_t m0v) {
+    uint32_t saved;
+    if constexpr (HS == 1) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %5, %1, 0 offen lds\n\t"
+            "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %6, %2, 0 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(rk), "s"(rv), "s"(m0k), "s"(m0v), "v"(off[0]), "v"(off[1])
+            : "memory");
+    } else if constexpr (HS == 2) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %5, %1, 0 offen lds\n\t"
+            "buffer_load_dwordx4 %6, %1, 0 offen offset:1024 lds\n\t"
+            "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %7, %2, 0 offen lds\n\t"
+            "buffer_load_dwordx4 %8, %2, 0 offen offset:1024 lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(rk), "s"(rv), "s"(m0k), "s"(m0v), "v"(off[0]), "v"(off[2]), "v"(off[1]), "v"(off[3])
+            : "memory");
+    } else {
+        static_assert(HS == 4, "runs of 1, 2 or 4 segments");
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %5, %1, 0 offen lds\n\t"
+            "buffer_load_dwordx4 %6, %1, 0 offen offset:1024 lds\n\t"
+            "buffer_load_dwordx4 %7, %1, 0 offen offset:2048 lds\n\t"
+            "buffer_load_dwordx4 %8, %1, 0 offen offset:3072 lds\n\t"
+            "s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+            "buffer_load_dwordx4 %9, %2, 0 offen lds\n\t"
+            "buffer_load_dwordx4 %10, %2, 0 offen offset:1024 lds\n\t"
+            "buffer_load_dwordx4 %11, %2, 0 offen offset:2048 lds\n\t"
+            "buffer_load_dwordx4 %12, %2, 0 offen offset:3072 lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(rk), "s"(rv), "s"(m0k), "s"(m0v), "v"(off[0]), "v"(off[2]), "v"(off[4]), "v"(off[6]),
+              "v"(off[1]), "v"(off[3]), "v"(off[5]), "v"(off[7])
+            : "memory");
+    }
+}
+
 // The running maximum (log2 units) is raised only when a block's maximum exceeds it by more than
 // this, so unnormalised probabilities stay below 2^12 and the rescale of the accumulators is rare.
 constexpr float kPrefillRescaleLog2 = 12.0f;
@@ -165,15 +216,26 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
     const char* kc = static_cast<const char*>(a.k_cache);
     const char* vc = static_cast<const char*>(a.v_cache);
 
-    // This wave's loads of a pair: segment k is 64-chunk segment wave + 4k of the pair's tiles
-    // (block 0 K, block 0 V, block 1 K, block 1 V). Lane l fills LDS position s0 + l of its tile
-    // and therefore loads the memory chunk the layout puts there.
-    int seg_off[NSEG];  // byte offset of this lane's chunk in its tile's memory
+    // This wave's loads of a pair. The pair's 64-chunk segments are ordered block by block, K and
+    // V alternating (K seg 0, V seg 0, K seg 1, ..); wave w loads the NSEG of them from w NSEG on:
+    // with two or more segments per tile, the same segments of one block's K and V tiles, so one
+    // block id, one tile offset and two descriptors serve all of a wave's loads. Lane l fills LDS
+    // position 64 i + l of segment i of its tile and therefore loads the memory chunk the layout
+    // puts there.
+    constexpr int HS = NSEG >= 2 ? NSEG / 2 : 1;  // segments per tile and wave
+    const int seg_blk = (wave * NSEG) / (2 * TL::SPT);            // the wave's block of the pair
+    const int seg_v0 = NSEG >= 2 ? 0 : wave & 1;                   // one segment per wave: K or V
+    const int seg_i0 = ((wave * NSEG) % (2 * TL::SPT)) >> 1;       // its first segment of the tile
+    // Loads of one tile issue from one LDS base (M0): segment j of the wave's run sits 1024 bytes
+    // further in LDS and in the load's immediate offset, which the hardware adds to both
+    // addresses, so the lane's register offset for it is its chunk's offset less 1024 j.
+    uint32_t seg_off[NSEG];  // k = 2j (K) and 2j + 1 (V) for NSEG >= 2; k = 0 otherwise
 #pragma unroll
     for (int k = 0; k < NSEG; k++) {
-        const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT, b = t >> 1;
-        const int pos = (sg % TL::SPT) * 64 + lane;
-        seg_off[k] = 16 * ((t & 1) ? TL::vsrc(pos, b) : TL::ksrc(pos));
+        const int j = NSEG >= 2 ? k >> 1 : 0;
+        const bool is_v = NSEG >= 2 ? (k & 1) : seg_v0;
+        const int pos = (seg_i0 + j) * 64 + lane;
+        seg_off[k] = 16 * (is_v ? TL::vsrc(pos, seg_blk) : TL::ksrc(pos)) - 1024 * j;
     }
     // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS.
     constexpr int KCH = D > 64 ? 512 : 1024;  // 3 workgroups per CU at D = 128 fit the LDS with 512
@@ -196,20 +258,18 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         }
         return __builtin_amdgcn_readlane(ids_v, j & 63);
     };
+    const uint32_t seg_lds = tile_lds + 16 * (TL::base(0, seg_blk) + 64 * seg_i0);  // the K run in slot 0
     auto issue = [&](int jl, int nkc, int slot) {
-        int id[2];
-        int64_t tile[2];
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            id[b] = block_id(jl + b, nkc);
-            tile[b] = (static_cast<int64_t>(id[b] >= 0 ? id[b] : 0) * Hkv + kvh) * TILE * ELT;
-        }
-#pragma unroll
-        for (int k = 0; k < NSEG; k++) {
-            const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT, b = t >> 1;
-            const u32x4_t rsrc = buffer_rsrc_words(((t & 1) ? vc : kc) + tile[b], id[b] >= 0 ? TILE * ELT : 0);
-            const int lpos = TL::base(slot, b) + ((t & 1) ? TL::K_CHUNKS : 0) + (sg % TL::SPT) * 64;
-            lds_load16(rsrc, seg_off[k], tile_lds + 16 * lpos);
+        const int id = block_id(jl + seg_blk, nkc);
+        const int64_t tile = (static_cast<int64_t>(id >= 0 ? id : 0) * Hkv + kvh) * TILE * ELT;
+        const uint32_t bytes = id >= 0 ? TILE * ELT : 0;
+        const uint32_t m0k = seg_lds + 16 * TL::SLOT * slot;
+        if constexpr (NSEG >= 2) {
+            lds_load_runs<HS>(buffer_rsrc_words(kc + tile, bytes), buffer_rsrc_words(vc + tile, bytes), seg_off, m0k,
+                              m0k + 16 * TL::K_CHUNKS);
+        } else {
+            lds_load16(buffer_rsrc_words((seg_v0 ? vc : kc) + tile, bytes), seg_off[0],
+                       m0k + (seg_v0 ? 16 * TL::K_CHUNKS : 0));
         }
     };
 
@@ -285,9 +345,9 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         auto convert_v = [&](int slot) {
 #pragma unroll
             for (int k = 0; k < NSEG; k++) {
-                const int sg = wave + kPrefillWaves * k, t = sg / TL::SPT;
-                if (t & 1) {
-                    uint4* c = s_tile + (TL::base(slot, t >> 1) + TL::K_CHUNKS + (sg % TL::SPT) * 64 + lane);
+                if (NSEG >= 2 ? (k & 1) : seg_v0) {
+                    const int j = NSEG >= 2 ? k >> 1 : 0;
+                    uint4* c = s_tile + (TL::base(slot, seg_blk) + TL::K_CHUNKS + (seg_i0 + j) * 64 + lane);
                     const uint4 x = *c;
                     const uint32_t w[4] = {x.x, x.y, x.z, x.w};
                     uint32_t o[4];
