@@ -532,6 +532,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C3/C4/C5 measurements")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time the C3 chunked prefill call only and print its own JSON line: for profiling")
+    ap.add_argument("--only-c3", action="store_true",
+                    help="time the C3 calls (decode, chunk append, prefill) alone and as one step, print their JSON line")
     ap.add_argument("--only-c5", action="store_true",
                     help="time C5 through pa_paged_decode and pa_paged_decode_prefix and print their JSON line")
     ap.add_argument("--only-layer", action="store_true",
@@ -575,6 +577,10 @@ def main():
         print(json.dumps({"mode": "only-c4", "workload": "C4 int8 fused append + decode", **c4,
                           "steps": args.steps}), flush=True)
         copy_calibration(args, stream)
+        return
+    if args.only_c3:
+        c3 = run_c3(timer, stream, args.steps, args.warmup, 3)
+        print(json.dumps({"mode": "only-c3", "workload": "C3 mixed step", **c3, "steps": args.steps}), flush=True)
         return
     if args.only_c5:
         w5 = wl.make_c5()
