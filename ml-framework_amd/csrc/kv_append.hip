@@ -309,7 +309,7 @@ pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, c
     const bool aligned = ((reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new) |
                            reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) % 16 == 0) &&
                          (tok_stride * (in_bf16 ? 2 : 4)) % 16 == 0;
-    if (cfg->kv_dtype != PA_DTYPE_INT8 && aligned) {
+    if (cfg->kv_dtype != PA_DTYPE_INT8 && aligned && cfg->num_kv_heads <= 65535) {  // grid y: one row per KV head
         const dim3 grid((n_tok + 15) / 16, cfg->num_kv_heads);
         const bool cb = cfg->kv_dtype == PA_DTYPE_BF16;
         auto go = [&](auto kern) {
