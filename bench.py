@@ -588,6 +588,7 @@ def main():
         shared = run_prefix_decode(w5, timer, stream, args.steps, args.warmup, 5)
         print(json.dumps({"mode": "only-c5", "workload": "C5 decode", "pa_paged_decode": plain,
                           "pa_paged_decode_prefix": shared, "steps": args.steps}), flush=True)
+        copy_calibration(args, stream)
         return
     if args.only_layer:
         lay = run_layer(timer, stream, w, inp, args.steps, args.warmup, 5)
