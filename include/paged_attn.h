@@ -193,14 +193,16 @@ pa_status pa_build_slot_mapping(pa_stream* stream, const pa_config* cfg,
 /* KV append / scatter (fills PagedAttentionLayer.UpdateKVCache/CopyTensorToBlock,
  * Layers/PagedAttentionLayer.cs:244-327, which is a no-op in the reference).
  * k_new, v_new: [n_tok][num_kv_heads][head_dim] of cfg->q_dtype (FP32 or BF16).
- * slot_mapping: [n_tok] int64, -1 = skip. Slots must be < num_blocks * block_size.
+ * slot_mapping: [n_tok] int64, -1 = skip. Slots must be < num_blocks * block_size (others are
+ *   skipped) and distinct: two new tokens of one call at one slot race.
  * FP32/BF16 caches store the converted value (fp32 -> bf16 truncates).
  * INT8 caches keep, per (block, KV head), an fp32 running absmax and scale = absmax / 127.
  *   Per call, the new tokens of one block raise absmax to max(absmax, max|x_new|); when it grows,
  *   every other slot of that block is requantised from q * old_scale with the new scale, then
  *   the new tokens are quantised with it. Quantisation is QuantizeSymmetric
  *   (src/MLFramework/Quantization/Operations/QuantizationOperations.cs:188-200).
- *   All new tokens that land in one block must be consecutive in the token list of a call.
+ *   A block's new tokens may sit anywhere in the call's token list (split by other blocks'
+ *   tokens or invalid slots); its segments (maximal runs of them) are applied in call order.
  *   k_scale/v_scale/k_absmax/v_absmax are required for INT8 and ignored otherwise. */
 pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg,
                        const void* k_new, const void* v_new,
