@@ -71,6 +71,7 @@ CHUNK = [33, 1, 16, 17, 100, 64, 5, 130]
 @pytest.mark.parametrize("flags", [0, pa.PA_FLAG_REFERENCE_LITERAL_MASK, pa.PA_FLAG_NO_MASK])
 @pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [
     (1, 1, 32, 8, 128), (1, 0, 8, 8, 64), (2, 1, 16, 2, 128), (2, 0, 8, 1, 64), (1, 1, 8, 4, 256),
+    (2, 1, 8, 2, 256),
 ])
 def test_prefill_ragged(stream, flags, kv_dtype, q_dtype, Hq, Hkv, D):
     got, ref = run_prefill(stream, prefix=PREFIX, chunk=CHUNK, Hq=Hq, Hkv=Hkv, D=D, kv_dtype=kv_dtype,
