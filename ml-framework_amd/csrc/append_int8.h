@@ -44,25 +44,38 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
     for (int o = 1; o < 64; o <<= 1) written |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(written), o, 64));
     const bool fresh = (written & 1u) != 0;
     const int64_t sidx = blk * num_kv_heads + h;
-    // The block's statistics are loaded with the segment's values (one round trip for both).
-    const float amax_mem = have_stats ? 0.0f : absmax[sidx];
-    const float scale_mem = have_stats ? 0.0f : scale[sidx];
-    float seg_amax = 0.0f;
-    for (int t = s; t < e; t++) {
-        const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
-#pragma unroll
-        for (int k = 0; k < kPer; k++) {
-            const float a = fabsf(load_act(src, in_bf16, base + lane + 64 * k));
-            seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
-        }
-    }
-    seg_amax = wave_max(seg_amax);
-
     int8_t* block_codes = cache + ((blk * num_kv_heads + h) * kBlockSize) * D;
     // Element (row off, dim d) of the tile: K is [16][D], V is [D][16].
     auto at = [&](int off, int d) -> int8_t* {
         return is_v ? block_codes + d * kBlockSize + off : block_codes + off * D + d;
     };
+    // One round trip for everything the segment reads: the block's statistics, its codes (needed
+    // only if the scale grows, so fetched unless the segment starts the block) as 16-byte chunks
+    // of the tile (chunk c of lane: c = lane + 64 i, K row c / (D/16) or V dim c), and, for a
+    // one-token segment, the token's values (kept for its quantisation).
+    const float amax_mem = have_stats ? 0.0f : absmax[sidx];
+    const float scale_mem = have_stats ? 0.0f : scale[sidx];
+    constexpr int kChunks = kBlockSize * D / 16 / 64;  // 16-byte chunks of the tile per lane
+    uint4 old_chunk[kChunks];
+    if (!fresh) {
+#pragma unroll
+        for (int i = 0; i < kChunks; i++) old_chunk[i] = reinterpret_cast<const uint4*>(block_codes)[lane + 64 * i];
+    }
+    const bool one = e - s == 1;
+    float x1[kPer];
+    float seg_amax = 0.0f;
+    for (int t = s; t < e; t++) {
+        const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            const float x = load_act(src, in_bf16, base + lane + 64 * k);
+            if (t == s) x1[k] = x;
+            const float a = fabsf(x);
+            seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
+        }
+    }
+    seg_amax = wave_max(seg_amax);
+
     if (fresh) {
         // Writing row 0 starts the block: earlier contents and statistics are discarded.
         amax = seg_amax;
@@ -81,16 +94,26 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
             cur_scale = seg_amax / 127.0f;
             amax = seg_amax;
             // Requantise every row this segment does not overwrite:
-            // QuantizeSymmetric(Dequantize(q, old_scale), new_scale).
-            for (int off = 0; off < kBlockSize; off++) {
-                if (written & (1u << off)) continue;
+            // QuantizeSymmetric(Dequantize(q, old_scale), new_scale). The rows it writes keep
+            // their old codes here; its own stores below replace them, after these have landed.
 #pragma unroll
-                for (int k = 0; k < kPer; k++) {
-                    int8_t* c = at(off, lane + 64 * k);
-                    const float deq = static_cast<float>(static_cast<int32_t>(*c)) * old_scale;
-                    *c = quantize_symmetric(deq, cur_scale);
+            for (int i = 0; i < kChunks; i++) {
+                const int c = lane + 64 * i;
+                uint32_t w[4] = {old_chunk[i].x, old_chunk[i].y, old_chunk[i].z, old_chunk[i].w};
+#pragma unroll
+                for (int b = 0; b < 16; b++) {
+                    const int row = is_v ? b : c / (D / 16);
+                    if (written & (1u << row)) continue;
+                    const uint32_t sh = 8 * (b & 3);
+                    const int32_t q = static_cast<int32_t>(w[b >> 2] << (24 - sh)) >> 24;
+                    const float deq = static_cast<float>(q) * old_scale;
+                    const uint32_t nq = static_cast<uint32_t>(static_cast<uint8_t>(quantize_symmetric(deq, cur_scale)));
+                    w[b >> 2] = (w[b >> 2] & ~(0xffu << sh)) | (nq << sh);
                 }
+                reinterpret_cast<uint4*>(block_codes)[c] = make_uint4(w[0], w[1], w[2], w[3]);
             }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile's stores precede the new rows'
+
             if (lane == 0) {
                 absmax[sidx] = amax;
                 scale[sidx] = cur_scale;
@@ -103,7 +126,7 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
         const int64_t base = static_cast<int64_t>(t) * tok_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
         for (int k = 0; k < kPer; k++) {
-            const float x = load_act(src, in_bf16, base + lane + 64 * k);
+            const float x = one ? x1[k] : load_act(src, in_bf16, base + lane + 64 * k);
             *at(off, lane + 64 * k) = quantize_symmetric(x, cur_scale);
         }
     }
