@@ -15,8 +15,11 @@
 //
 // A portion is streamed in pieces of at most 64 blocks (lane j holds the id of the piece's block
 // j); the running (max, sum, O) carry over from piece to piece and are written when the portion
-// ends. The next piece's ids are loaded while the current one streams, so a piece starts with one
-// memory round trip.
+// ends. Block ids are loaded two pieces ahead. Kernels without the fused append (and with bf16
+// queries, head_dim <= 128) also carry the pipeline across pieces: a piece issues the next one's
+// Q and scales at its start and its first two blocks in its last two iterations, so a piece or
+// row boundary does not drain the blocks in flight. The others start a piece with its own loads
+// (one memory round trip).
 //
 // Per block: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads padded
 // to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
@@ -95,18 +98,175 @@ struct RowState {
     }
 };
 
-// One piece, streamed by one wave; my_bid = piece_ids(..). prefetch_next() is called once, after
-// the piece's first loads, to start the next piece's id loads. s_new: this wave's LDS staging of
-// the appended token (2 * D floats).
+// Values a piece needs besides its K/V blocks: Q (lane (q4, n): head n's dims of each slab, bf16
+// words, or fp32 values in two 16-byte words per slab), the int8 scales of the lane's block (lane
+// j: block j of the piece) and the appended token's raw bits.
+template <int D, bool QF32>
+struct PieceSide {
+    static constexpr int NPL = D >= 64 ? D / 64 : 1;  // appended-token values per lane
+    static constexpr int NW = QF32 ? NPL : (NPL + 1) / 2;
+    uint4 q[QF32 ? D / 16 : D / 32];
+    float ks, vs;
+    uint32_t nk[NW], nv[NW];
+};
+
+// The three rotating register buffers of a wave's block pipeline (two blocks in flight while a
+// third is consumed). They outlive a piece: the last iterations of one piece load the first two
+// blocks of the next (carry), so a piece boundary does not drain the pipeline.
+template <int D, int KV>
+struct PipeBufs {
+    typename MfmaRaw<KV>::K k[3][D / 32];
+    typename MfmaRaw<KV>::V v[3][D / 16];
+};
+
+// Vector memory instructions load_block issues per block.
+template <int D, int KV>
+__host__ __device__ constexpr int decode_block_loads() {
+    return (KV == PA_DTYPE_INT8 ? D / 64 : D / 32) + D / 16;
+}
+// s_waitcnt operand: wait until at most N vector memory operations are outstanding (no wait on
+// the other counters).
+template <int N>
+__host__ __device__ constexpr int vmcnt_keep() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    return (N & 15) | 0x7 << 4 | 0xf << 8 | (N >> 4) << 14;
+}
+
+// Carry across pieces (bf16 queries, head_dim <= 128, no fused append): elsewhere the extra
+// registers (the next piece's Q) would spill, so those kernels start every piece with its own loads.
+template <int D, int KV, bool QF32, bool APPEND>
+__host__ __device__ constexpr bool decode_carry() {
+    return decode_buffers(KV) == 3 && !QF32 && !APPEND && D <= 128;
+}
+
+// Fused append: the row's last block is entry j_app of the piece that ends the row (-1: none).
+template <bool APPEND>
+__device__ __forceinline__ int piece_app(const Piece& g) {
+    if constexpr (!APPEND) return -1;
+    const int nbrow = (g.T + 15) / 16;
+    return g.b1 == nbrow ? nbrow - 1 - g.b0 : -1;
+}
+// List entry consumed by iteration j of a piece: the appended block first (its patch then happens
+// while the pipeline fills), then the others in order.
+__device__ __forceinline__ int piece_entry(int j_app, int j) { return j_app > 0 ? (j == 0 ? j_app : j - 1) : j; }
+
+// Side loads of piece g (ids: its block ids, lane j = block j): Q, the appended token and, when
+// `scales`, the int8 scales (those need the ids, which may still be in flight).
+template <int D, int KV, bool QF32, bool APPEND, bool SHARED>
+__device__ __forceinline__ void load_side(const DecodeArgs& a, const Piece& g, int ids, bool scales,
+                                          PieceSide<D, QF32>& sd) {
+    constexpr int NSLAB = D / 32;
+    constexpr int NPL = PieceSide<D, QF32>::NPL;
+    constexpr int NW = PieceSide<D, QF32>::NW;
+    const int lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, n = lane & 15;
+    const int G = a.group, Hkv = a.num_kv_heads;
+    // Column n's query head: head n of the sequence, or (shared-prefix rows) head n % G of member
+    // n / G.
+    const int ncol = SHARED ? g.nmem * G : G;
+    const bool hv = n < ncol;
+    const int mi = SHARED && hv ? n / G : 0;
+    const int64_t qrow = (static_cast<int64_t>(g.seq + mi) * Hkv * G + g.kvh * G + (hv ? n - mi * G : 0)) * D;
+    // Every lane loads (a lane without a head reads head 0 of the row, which exists); the consumer
+    // zeroes the columns without a head when it builds the operands (masking here would wait for
+    // the load at its issue; a conditional load is compiled into a pointer select through a stack
+    // copy).
+#pragma unroll
+    for (int s = 0; s < NSLAB; s++) {
+        const int d0 = k_dim0<D, KV>(s, q4);
+        if constexpr (QF32) {
+            const uint4* qp = reinterpret_cast<const uint4*>(static_cast<const float*>(a.q) + qrow + d0);
+            sd.q[2 * s] = qp[0];
+            sd.q[2 * s + 1] = qp[1];
+        } else {
+            sd.q[s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0);
+        }
+    }
+    if constexpr (KV == PA_DTYPE_INT8) {  // unconditional: an invalid block's scales are never used
+        if (scales) {
+            const int sb = ids >= 0 && ids < a.num_blocks ? ids : 0;
+            sd.ks = a.k_scale[static_cast<int64_t>(sb) * Hkv + g.kvh];
+            sd.vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + g.kvh];
+        }
+    }
+    if constexpr (APPEND) {
+        if (piece_app<APPEND>(g) >= 0 && lane * NPL < D) {
+            const int64_t src = (static_cast<int64_t>(g.seq) * Hkv + g.kvh) * D + lane * NPL;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                if constexpr (QF32) {
+                    sd.nk[w] = static_cast<const uint32_t*>(a.k_new)[src + w];
+                    sd.nv[w] = static_cast<const uint32_t*>(a.v_new)[src + w];
+                } else if constexpr (NPL == 1) {
+                    sd.nk[w] = static_cast<const uint16_t*>(a.k_new)[src];
+                    sd.nv[w] = static_cast<const uint16_t*>(a.v_new)[src];
+                } else {
+                    sd.nk[w] = static_cast<const uint32_t*>(a.k_new)[(src >> 1) + w];
+                    sd.nv[w] = static_cast<const uint32_t*>(a.v_new)[(src >> 1) + w];
+                }
+            }
+        }
+    }
+}
+
+// Loads of block bid (K/V tile of KV head kv) into a pipeline buffer, lane (q4, n): K row n (the
+// lane's dims of each slab), V dim n of tokens 4q4 .. 4q4 + 3 (every 16th dim). Loads go through
+// per-block buffer descriptors: bid < 0 (past a list, or an invalid id) gives a zero-sized
+// descriptor, so its loads return zeros without touching memory. The load sequence is therefore
+// identical on every iteration (no branches), which lets the compiler wait for exactly the oldest
+// block instead of draining every load in flight.
+template <int D, int KV>
+__device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw<KV>::K (&kr)[D / 32],
+                                           typename MfmaRaw<KV>::V (&vr)[D / 16], int bid, int kv) {
+    using KR = typename MfmaRaw<KV>::K;
+    using VR = typename MfmaRaw<KV>::V;
+    constexpr int ELT = MfmaRaw<KV>::kElt;
+    constexpr int NSLAB = D / 32, NT = D / 16, TILE = 16 * D;
+    constexpr int kLoadCP = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
+    const int lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, n = lane & 15;
+    const int k_row_off = n * D * ELT;               // K row n; slab s of this lane starts at dim k_dim0(s, q4)
+    const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
+    const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * a.num_kv_heads + kv) * TILE * ELT : 0;
+    const int bytes = bid >= 0 ? TILE * ELT : 0;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(a.k_cache) + tile), 0, bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(a.v_cache) + tile), 0, bytes, kBufferFlags);
+    if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
+#pragma unroll
+        for (int s = 0; s < NSLAB; s += 2) {
+            const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4));
+            kr[s] = make_uint2(w.x, w.y);
+            kr[s + 1] = make_uint2(w.z, w.w);
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kLoadCP>(rv, v_lane_off + 256 * t * ELT);
+}
+
+// One piece, streamed by one wave; my_bid = piece_ids(..). has_next, nxt, nxt_ids: the next piece
+// of the worker and its block ids (loaded during the previous piece). With carry
+// (decode_carry()), the piece's first two blocks and side loads were issued before it (by the
+// previous piece, or for a worker's first piece by the worker), and it issues the next piece's
+// side loads at its start and its first two blocks in its last two iterations. prefetch_next() is
+// called once, after the piece's first loads, to start the id loads of the piece after the next.
+// s_new: this wave's LDS staging of the appended token (2 * D floats).
 template <int D, int KV, bool QF32, bool APPEND, bool SHARED, typename Prefetch>
-__device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, int my_bid, RowState<D / 16>& st,
-                                           float* s_new, Prefetch&& prefetch_next) {
+__device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, int my_bid,
+                                           PieceSide<D, QF32>& side, PipeBufs<D, KV>& bufs, RowState<D / 16>& st,
+                                           float* s_new, const bool& has_next, const Piece& nxt, const int& nxt_ids,
+                                           PieceSide<D, QF32>& nside, Prefetch&& prefetch_next) {
     using Raw = MfmaRaw<KV>;
-    constexpr int ELT = Raw::kElt;
     constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
     constexpr int NT = D / 16;     // PV n-tiles of 16 dims
     constexpr int TILE = 16 * D;   // elements per (block, KV head) tile
-    constexpr int NPL = D >= 64 ? D / 64 : 1;  // appended-token values per lane (lanes < D when D = 32)
+    constexpr int NPL = PieceSide<D, QF32>::NPL;
+    constexpr int NW = PieceSide<D, QF32>::NW;
+    constexpr bool CARRY = decode_carry<D, KV, QF32, APPEND>();
 
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4;  // token group (QK C rows) / k group of the MFMA operands
@@ -114,28 +274,17 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     const int G = a.group, Hkv = a.num_kv_heads;
     const int seq = g.seq, kvh = g.kvh, T = g.T;
     const int nb = g.b1 - g.b0;
-    const int nbrow = (T + 15) / 16;
 
-    // Loads issued at the piece's start, in this order: its first two K/V blocks, the next
-    // piece's block ids (prefetch callback), then Q, the int8 block scales and the appended token.
-    // Memory returns in order, so the K/V requests go out first; none of the other values is
+    // Loads issued at the piece's start, in this order: its first two K/V blocks and its side loads
+    // (without carry), the ids of the piece after the next (prefetch callback) and the next piece's
+    // side loads (with carry). Memory returns in order, so the K/V requests go out first; none of the other values is
     // used right after its load (that would stall the wave on the load's latency).
-    float my_ks = 0.0f, my_vs = 0.0f;  // int8: scales of this lane's block
-    // Fused append (bf16 caches; int8 caches are appended by a separate launch first): the row's
-    // last block is entry nbrow - 1 - b0 of the piece that ends the row. Its wave fetches the new
-    // token (lane l: dims l*NPL ..); the token's raw bits (fp32, or bf16 packed two per word) are
-    // decoded only at the patch.
+    // Fused append (bf16 caches; int8 caches are appended by a separate launch first): the wave
+    // that streams the row's last block fetches the new token (lane l: dims l*NPL ..); the token's
+    // raw bits (fp32, or bf16 packed two per word) are decoded only at the patch.
     static_assert(!(APPEND && KV == PA_DTYPE_INT8), "int8 caches are appended before the decode");
-    constexpr int NW = QF32 ? NPL : (NPL + 1) / 2;
-    int j_app = -1;
-    uint32_t nk_raw[NW], nv_raw[NW];
-    if constexpr (APPEND) {
-        if (g.b1 == nbrow) j_app = nbrow - 1 - g.b0;  // always the piece's last block
-    }
-    // That piece consumes its blocks starting with the last one (iteration 0 takes list entry
-    // j_app, iteration j takes entry j - 1): the patch then happens while the pipeline fills.
-    const bool rot = APPEND && j_app > 0;
-    auto entry = [&](int j) { return rot ? (j == 0 ? j_app : j - 1) : j; };
+    const int j_app = piece_app<APPEND>(g);
+    auto entry = [&](int j) { return piece_entry(j_app, j); };
     auto new_val = [&](const uint32_t (&raw)[NW], int e) -> float {
         if constexpr (QF32) return __uint_as_float(raw[e]);
         else if constexpr (NPL == 1) return __uint_as_float(raw[0] << 16);
@@ -181,117 +330,83 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             qdl[t] = __builtin_bit_cast(i32x4_t, make_uint4(wl[0], wl[1], wl[2], wl[3]));
         }
     };
-    // Column n's query head: head n of the sequence, or (shared-prefix rows) head n % G of member
-    // n / G.
     const int ncol = SHARED ? g.nmem * G : G;
-    auto side_loads = [&]() {
-        const bool hv = n < ncol;
-        const int mi = SHARED && hv ? n / G : 0;
-        const int64_t qrow =
-            (static_cast<int64_t>(seq + mi) * Hkv * G + kvh * G + (hv ? n - mi * G : 0)) * D;
+    // Q words of the side loads, zero in the columns without a head (n >= ncol).
+    const uint32_t qmask = n < ncol ? 0xffffffffu : 0u;
+    auto qword = [&](int i) {
+        const uint4 w = side.q[i];
+        return make_uint4(w.x & qmask, w.y & qmask, w.z & qmask, w.w & qmask);
+    };
+    // Slab s of Q as 8 floats.
+    auto q_floats = [&](int s, float (&x)[8]) {
+        if constexpr (QF32) {
+            const uint4 w0 = qword(2 * s), w1 = qword(2 * s + 1);
+            const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = __uint_as_float(w[e]);
+        } else {
+            const uint4 raw = qword(s);
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+        }
+    };
+    // Q operands from the side loads.
+    auto prep_q = [&]() {
         if constexpr (KV == PA_DTYPE_INT8) {
             float x[NSLAB][8];
 #pragma unroll
-            for (int s = 0; s < NSLAB; s++) {
-                const int d0 = k_dim0<D, KV>(s, q4);
-                if constexpr (QF32) {
-                    const float* qp = static_cast<const float*>(a.q) + qrow + d0;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[s][e] = hv ? qp[e] : 0.0f;
-                } else {
-                    const uint4 raw = hv ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
-                                         : make_uint4(0, 0, 0, 0);
-                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        x[s][e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
-                }
-            }
+            for (int s = 0; s < NSLAB; s++) q_floats(s, x[s]);
             int8_q_digits(x);
         } else {
 #pragma unroll
-        for (int s = 0; s < NSLAB; s++) {
-            const int d0 = k_dim0<D, KV>(s, q4);
-            if constexpr (QF32) {
-                const float* qp = static_cast<const float*>(a.q) + qrow + d0;
-                float x[8];
+            for (int s = 0; s < NSLAB; s++) {
+                if constexpr (QF32) {
+                    float x[8];
+                    q_floats(s, x);
+                    uint32_t h[4], l[4];
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = hv ? qp[e] : 0.0f;
-                uint32_t h[4], l[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    h[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
-                    const float r0 = x[2 * e] - __uint_as_float(__float_as_uint(x[2 * e]) & 0xffff0000u);
-                    const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
-                    l[e] = pack_bf16_trunc(r0, r1);
-                }
-                qhi[s] = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
-                qlo[s] = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
-            } else {
-                const uint4 raw = hv ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.q) + qrow + d0)
-                                     : make_uint4(0, 0, 0, 0);
-                qhi[s] = __builtin_bit_cast(bf16x8_t, raw);
-            }
-        }
-        }
-        if constexpr (KV == PA_DTYPE_INT8) {  // unconditional: an invalid block's scales are never used
-            const int sb = my_bid >= 0 && my_bid < a.num_blocks ? my_bid : 0;
-            my_ks = a.k_scale[static_cast<int64_t>(sb) * Hkv + kvh];
-            my_vs = a.v_scale[static_cast<int64_t>(sb) * Hkv + kvh];
-        }
-        if constexpr (APPEND) {
-            if (j_app >= 0 && lane * NPL < D) {
-                const int64_t src = (static_cast<int64_t>(seq) * Hkv + kvh) * D + lane * NPL;
-#pragma unroll
-                for (int w = 0; w < NW; w++) {
-                    if constexpr (QF32) {
-                        nk_raw[w] = static_cast<const uint32_t*>(a.k_new)[src + w];
-                        nv_raw[w] = static_cast<const uint32_t*>(a.v_new)[src + w];
-                    } else if constexpr (NPL == 1) {
-                        nk_raw[w] = static_cast<const uint16_t*>(a.k_new)[src];
-                        nv_raw[w] = static_cast<const uint16_t*>(a.v_new)[src];
-                    } else {
-                        nk_raw[w] = static_cast<const uint32_t*>(a.k_new)[(src >> 1) + w];
-                        nv_raw[w] = static_cast<const uint32_t*>(a.v_new)[(src >> 1) + w];
+                    for (int e = 0; e < 4; e++) {
+                        h[e] = pack_bf16_trunc(x[2 * e], x[2 * e + 1]);
+                        const float r0 = x[2 * e] - __uint_as_float(__float_as_uint(x[2 * e]) & 0xffff0000u);
+                        const float r1 = x[2 * e + 1] - __uint_as_float(__float_as_uint(x[2 * e + 1]) & 0xffff0000u);
+                        l[e] = pack_bf16_trunc(r0, r1);
                     }
+                    qhi[s] = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+                    qlo[s] = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+                } else {
+                    qhi[s] = __builtin_bit_cast(bf16x8_t, qword(s));
                 }
             }
         }
     };
 
-    const char* kc = static_cast<const char*>(a.k_cache);
-    const char* vc = static_cast<const char*>(a.v_cache);
+    // The next piece (carry): its block count and this piece's padded iteration count nbp, the
+    // smallest multiple of 3 >= max(nb, 3). Iterations nb .. nbp - 1 compute nothing; item nbp + k
+    // is the next piece's block k, loaded into buffer (nbp + k) % 3 = k, where the next piece reads
+    // it. The next piece's side loads go out at this piece's start (its ids were loaded during the
+    // previous piece).
+    const int nbp = CARRY ? (max(nb, 3) + 2) / 3 * 3 : nb;
+    const int nnb = CARRY && has_next ? nxt.b1 - nxt.b0 : 0;
+    auto side_next = [&]() {
+        if constexpr (CARRY) {
+            if (has_next) load_side<D, KV, QF32, APPEND, SHARED>(a, nxt, nxt_ids, true, nside);
+        }
+    };
+
     using KR = typename Raw::K;
     using VR = typename Raw::V;
-    const int k_row_off = n * D * ELT;  // K row n; slab s of this lane starts at dim k_dim0(s, q4)
-    constexpr int kLoadCP = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
-    const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
-    // Loads go through per-block buffer descriptors: a block past the wave's list or with an
-    // invalid id gets a zero-sized descriptor, so its loads return zeros without touching memory.
-    // The load sequence is therefore identical on every iteration (no branches), which lets the
-    // compiler wait for exactly the oldest block instead of draining every load in flight.
-    auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
-        const int bid = j < nb ? valid_bid(a, __builtin_amdgcn_readlane(my_bid, entry(j) & 63)) : -1;
-        const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * Hkv + kvh) * TILE * ELT : 0;
-        const int bytes = bid >= 0 ? TILE * ELT : 0;
-        const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kc + tile), 0, bytes, kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vc + tile), 0, bytes, kBufferFlags);
-        if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
-#pragma unroll
-            for (int s = 0; s < NSLAB; s += 2) {
-                const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4));
-                kr[s] = make_uint2(w.x, w.y);
-                kr[s + 1] = make_uint2(w.z, w.w);
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < NSLAB; s++)
-                kr[s] = buffer_load<KR, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
+    // Item i: block entry(i) of this piece (i < nb), nothing (nb <= i < nbp) or block i - nbp of
+    // the next piece (zero-sized past its list).
+    auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int i) {
+        int bid = -1, kv = kvh;
+        if (i < nb) {
+            bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, entry(i) & 63));
+        } else if (CARRY && i >= nbp && i - nbp < nnb) {
+            bid = valid_bid(a, __builtin_amdgcn_readlane(nxt_ids, i - nbp));
+            kv = nxt.kvh;
         }
-#pragma unroll
-        for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kLoadCP>(rv, v_lane_off + 256 * t * ELT);
+        load_block<D, KV>(a, kr, vr, bid, kv);
     };
 
     float& m_run = st.m_run;
@@ -304,8 +419,8 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         const int bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, e));
         float ks = 1.0f, vfac = 1.0f;
         if constexpr (KV == PA_DTYPE_INT8) {
-            ks = bid >= 0 ? readlane_f(my_ks, e) : 0.0f;
-            vfac = bid >= 0 ? readlane_f(my_vs, e) : 0.0f;
+            ks = bid >= 0 ? readlane_f(side.ks, e) : 0.0f;
+            vfac = bid >= 0 ? readlane_f(side.vs, e) : 0.0f;
         }
         if constexpr (APPEND) {
             if (app && e == j_app && bid >= 0) {
@@ -315,8 +430,8 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                 uint32_t kw[NW], vw[NW];
 #pragma unroll
                 for (int w = 0; w < NW; w++) {
-                    kw[w] = nk_raw[w];
-                    vw[w] = nv_raw[w];
+                    kw[w] = side.nk[w];
+                    vw[w] = side.nv[w];
                     asm volatile("" : "+v"(kw[w]), "+v"(vw[w]));
                 }
                 if (lane * NPL < D) {
@@ -423,14 +538,15 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
 
     if constexpr (decode_buffers(KV) != 3) {
         // NB rotating register buffers: NB - 1 blocks in flight while one is consumed (int8 blocks
-        // carry half the bytes of bf16 ones, so more of them are kept in flight).
+        // carry half the bytes of bf16 ones, so more of them are kept in flight). No carry.
         constexpr int NB = decode_buffers(KV);
         KR kbuf[NB][NSLAB];
         VR vbuf[NB][NT];
 #pragma unroll
         for (int i = 0; i < NB - 1; i++) load(kbuf[i], vbuf[i], i);
+        load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
         prefetch_next();
-        side_loads();
+        prep_q();
         int j = 0;
         while (j < nb) {
 #pragma unroll
@@ -441,44 +557,79 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             }
         }
     } else {
-        // Three rotating register buffers: two blocks in flight while a third is consumed. Loads
-        // past the wave's list are zero-sized (no memory traffic), so they are issued regardless.
-        KR ka[NSLAB], kb[NSLAB], kx[NSLAB];
-        VR va[NT], vb[NT], vx[NT];
+        // Three rotating register buffers (A, B, X = bufs 0, 1, 2): two blocks in flight while a
+        // third is consumed. Loads of items past the piece (or of the next piece's blocks past its
+        // list) are zero-sized (no memory traffic), so they are issued regardless.
+        auto& ka = bufs.k[0];
+        auto& kb = bufs.k[1];
+        auto& kx = bufs.k[2];
+        auto& va = bufs.v[0];
+        auto& vb = bufs.v[1];
+        auto& vx = bufs.v[2];
         int j = 0;
-        bool peeled = false;
-        if constexpr (APPEND) {
-            if (j_app >= 0) {
-                // Iteration 0 (the appended block) is computed here, outside the loop: with the
-                // patch inlined in the loop body the int8 loop no longer fits the instruction cache
-                // and every wave slows down. The loop then starts at iteration 1 with the same
-                // buffer roles as usual.
-                load(kx, vx, 0);
-                load(ka, va, 1);
-                load(kb, vb, 2);
-                prefetch_next();
-                side_loads();
-                compute(kx, vx, 0, true);
-                j = 1;
-                peeled = true;
-            }
-        }
-        if (!peeled) {
-            load(ka, va, 0);
-            load(kb, vb, 1);
+        if constexpr (CARRY) {
+            // Items 0, 1 are in A, B and the side loads in `side` (issued by the previous piece,
+            // or for a worker's first piece before it); the loop's last two iterations issue the
+            // next piece's first two blocks.
             prefetch_next();
-            side_loads();
-        }
-        while (j < nb) {
-            load(kx, vx, j + 2);
-            compute(ka, va, j, false);
-            if (++j >= nb) break;
-            load(ka, va, j + 2);
-            compute(kb, vb, j, false);
-            if (++j >= nb) break;
-            load(kb, vb, j + 2);
-            compute(kx, vx, j, false);
-            ++j;
+            side_next();
+            prep_q();
+            // The ids of this piece and the next were loaded a piece ago: wait for them here, not
+            // inside the loop (where a first use would make every iteration drain the loads).
+            asm volatile("" ::"v"(my_bid), "v"(nxt_ids));
+            do {
+                load(kx, vx, j + 2);
+                if (j < nb) compute(ka, va, j, false);
+                ++j;
+                load(ka, va, j + 2);
+                if (j < nb) compute(kb, vb, j, false);
+                ++j;
+                load(kb, vb, j + 2);
+                if (j < nb) compute(kx, vx, j, false);
+                ++j;
+            } while (j < nbp);
+            // Every vector memory access but the next piece's two blocks (the last 2 * LPI) has
+            // completed by now. Waiting on that explicitly (free) tells the compiler so: the ids
+            // and side values loaded before the loop are then known to be in registers, and the
+            // next piece does not drain its carried loads to use them.
+            __builtin_amdgcn_s_waitcnt(vmcnt_keep<2 * decode_block_loads<D, KV>()>());
+        } else {
+            bool peeled = false;
+            if constexpr (APPEND) {
+                if (j_app >= 0) {
+                    // Iteration 0 (the appended block) is computed here, outside the loop: with the
+                    // patch inlined in the loop body the loop no longer fits the instruction cache
+                    // and every wave slows down. The loop then starts at iteration 1 with the same
+                    // buffer roles as usual.
+                    load(kx, vx, 0);
+                    load(ka, va, 1);
+                    load(kb, vb, 2);
+                    load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
+                    prefetch_next();
+                    prep_q();
+                    compute(kx, vx, 0, true);
+                    j = 1;
+                    peeled = true;
+                }
+            }
+            if (!peeled) {
+                load(ka, va, 0);
+                load(kb, vb, 1);
+                load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
+                prefetch_next();
+                prep_q();
+            }
+            while (j < nb) {
+                load(kx, vx, j + 2);
+                compute(ka, va, j, false);
+                if (++j >= nb) break;
+                load(ka, va, j + 2);
+                compute(kb, vb, j, false);
+                if (++j >= nb) break;
+                load(kb, vb, j + 2);
+                compute(kx, vx, j, false);
+                ++j;
+            }
         }
     }
 
@@ -697,20 +848,45 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     RowState<D / 16> st;
     st.reset();
     float* s_new = &s_app[wave][0];
-    Piece cur;
+    PipeBufs<D, KV> bufs;
+    PieceSide<D, QF32> side, nside;
+    // Pieces in flight: cur (streaming), nxt (ids loaded during the previous piece) and nxt2 (ids
+    // loaded during this one).
+    Piece cur, nxt;
     next_piece(cur);
     int cur_ids = piece_ids(a, cur, lane);
+    bool has_next = next_piece(nxt);
+    int nxt_ids = has_next ? piece_ids(a, nxt, lane) : -1;
+    // The first piece waits for its ids anyway; waiting for both here lets the compiler treat the
+    // ids a piece receives as loaded on every path into the loop.
+    asm volatile("" ::"v"(cur_ids), "v"(nxt_ids));
+    if constexpr (decode_carry<D, KV, QF32, APPEND>()) {
+        // The first piece's carried loads: its side loads, then its first two blocks. Waiting for
+        // all but the blocks here puts the side values in registers on every path into the loop,
+        // so no later piece waits on them (with its carried blocks in flight).
+        const int nb0 = cur.b1 - cur.b0;
+        load_side<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, true, side);
+        load_block<D, KV>(a, bufs.k[0], bufs.v[0], valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 0)), cur.kvh);
+        load_block<D, KV>(a, bufs.k[1], bufs.v[1], nb0 > 1 ? valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 1)) : -1,
+                          cur.kvh);
+        __builtin_amdgcn_s_waitcnt(vmcnt_keep<2 * decode_block_loads<D, KV>()>());
+    }
     for (;;) {
-        Piece nxt;
-        bool has_next = false;
-        int nxt_ids = -1;
-        mfma_piece<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, st, s_new, [&]() {
-            has_next = next_piece(nxt);
-            if (has_next) nxt_ids = piece_ids(a, nxt, lane);  // in flight during this piece
-        });
+        Piece nxt2;
+        bool has_next2 = false;
+        int nxt2_ids = -1;
+        mfma_piece<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, side, bufs, st, s_new, has_next, nxt,
+                                                nxt_ids, nside, [&]() {
+                                                    if (has_next) has_next2 = next_piece(nxt2);
+                                                    if (has_next2) nxt2_ids = piece_ids(a, nxt2, lane);
+                                                });
         if (!has_next) break;
         cur = nxt;
         cur_ids = nxt_ids;
+        has_next = has_next2;
+        nxt = nxt2;
+        nxt_ids = nxt2_ids;
+        if constexpr (decode_carry<D, KV, QF32, APPEND>()) side = nside;
     }
 }
 
