@@ -340,6 +340,22 @@ def test_decode_edge_lengths(stream, part, kv_dtype, q_dtype, Hq, Hkv, D):
     assert np.all(got[0] == 0.0)  # context_len 0 -> zeros
 
 
+@pytest.mark.parametrize("part", [64, 0])
+@pytest.mark.parametrize("kv_dtype,q_dtype", [(1, 1), (2, 1), (2, 0)])
+def test_decode_many_short_rows(stream, kv_dtype, q_dtype, part):
+    """Hundreds of rows of 1 to 8 blocks: a worker's range crosses many row ends, so the pipeline
+    is carried across many pieces (a piece of 1 or 2 blocks still hands the next piece its first two
+    blocks). With a 4-block partition there are more units than workers, and with 3 KV heads a
+    worker's next unit belongs to another KV head."""
+    rng = np.random.default_rng(31 + kv_dtype)
+    lens = rng.integers(1, 161, size=1000).astype(np.int32)
+    lens[::37] = 16  # whole blocks
+    w = wl.make_small(41 + kv_dtype, num_seqs=len(lens), lens=lens, Hq=12, Hkv=3, D=128,
+                      kv_dtype=kv_dtype, q_dtype=q_dtype)
+    got, ref = run_decode(w, 59, stream, partition_size=part)
+    check_close(got, ref, **tol_for(kv_dtype), what=f"short rows kv={kv_dtype} part={part}")
+
+
 @pytest.mark.parametrize("part", [0, 4096])
 @pytest.mark.parametrize("kv_dtype", [1, 2])
 def test_decode_long_segments(stream, kv_dtype, part):
