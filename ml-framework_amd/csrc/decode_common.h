@@ -442,9 +442,9 @@ __device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t ti
 constexpr int kBufferFlags = 0x00020000;
 
 // CP: the load's cache-policy operand; kLoadNonTemporal marks data that is not read again soon.
-// Measured on the decode's K/V stream: int8 caches (C4) 143 -> 132 us with it, bf16 caches
-// slower (C2 66 -> 78 us, and C5, whose shared prefix is re-read from the last-level cache, 127 ->
-// 159 us), so only the int8 decode uses it.
+// Measured on the decode's K/V stream (us per step): int8 caches, K and V non-temporal, C4 136.0
+// -> 125.8; bf16 caches, V only: C2 over two pools 67.3 -> 58.6, C5 128.2 -> 123.9, C5 through
+// the shared-prefix decode 113.2 -> 99.5 (K and V: 61.9, 131.6, 108.8; K only: 63.2, 124.9).
 constexpr int kLoadDefault = 0;
 constexpr int kLoadNonTemporal = 2;
 template <typename T, int CP = kLoadDefault> __device__ __forceinline__ T buffer_load(__amdgpu_buffer_rsrc_t r, int off) {

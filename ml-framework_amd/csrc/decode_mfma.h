@@ -222,7 +222,10 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
     using VR = typename MfmaRaw<KV>::V;
     constexpr int ELT = MfmaRaw<KV>::kElt;
     constexpr int NSLAB = D / 32, NT = D / 16, TILE = 16 * D;
-    constexpr int kLoadCP = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
+    // Cache policy: non-temporal for V (each tile is read once) and, for int8 caches, for K too
+    // (bf16 K with it measured slower).
+    constexpr int kCPK = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
+    constexpr int kCPV = kLoadNonTemporal;
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4, n = lane & 15;
     const int k_row_off = n * D * ELT;               // K row n; slab s of this lane starts at dim k_dim0(s, q4)
@@ -236,16 +239,16 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
     if constexpr (ELT == 1) {  // int8: two slabs (16 codes) per 16-byte load
 #pragma unroll
         for (int s = 0; s < NSLAB; s += 2) {
-            const uint4 w = buffer_load<uint4, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4));
+            const uint4 w = buffer_load<uint4, kCPK>(rk, k_row_off + k_dim0<D, KV>(s, q4));
             kr[s] = make_uint2(w.x, w.y);
             kr[s + 1] = make_uint2(w.z, w.w);
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kLoadCP>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
+        for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kCPK>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
     }
 #pragma unroll
-    for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kLoadCP>(rv, v_lane_off + 256 * t * ELT);
+    for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kCPV>(rv, v_lane_off + 256 * t * ELT);
 }
 
 // One piece, streamed by one wave; my_bid = piece_ids(..). has_next, nxt, nxt_ids: the next piece
