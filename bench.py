@@ -107,10 +107,10 @@ def make_inputs(w: wl.Workload, seed: int):
     return out
 
 
-def config_of(w: wl.Workload, partition_size=0):
+def config_of(w: wl.Workload, partition_size=0, num_splits=0):
     return pa.make_config(num_q_heads=w.num_q_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
                           kv_dtype=w.kv_dtype, q_dtype=w.q_dtype, num_blocks=w.num_blocks,
-                          partition_size=partition_size)
+                          partition_size=partition_size, num_splits=num_splits)
 
 
 class Timer:
@@ -166,9 +166,9 @@ def append_bytes(w):
     return 2 * w.num_seqs * w.num_kv_heads * w.head_dim * (act + cache)
 
 
-def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
+def run_decode_config(w, timer, stream, steps, warmup, fused, seed, num_splits=0):
     inp = make_inputs(w, seed)
-    cfg = config_of(w)
+    cfg = config_of(w, num_splits=num_splits)
     out, ws, wsb = decode_buffers(w, cfg)
     ms = timer(decode_step(w, inp, stream, cfg, fused, out, ws, wsb), steps, warmup)
     nbytes = w.decode_algorithmic_bytes() + (append_bytes(w) if fused else 0)
@@ -176,7 +176,8 @@ def run_decode_config(w, timer, stream, steps, warmup, fused, seed):
     res = {"us_per_layer_step": round(ms * 1e3, 3), "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1),
            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "tokens_per_s_per_layer": round(w.num_seqs / (ms * 1e-3), 1),
            "context_tokens": int(w.context_lens.sum()), "num_seqs": w.num_seqs,
-           "step": "pa_paged_decode_append" if fused else "pa_paged_decode"}
+           "step": "pa_paged_decode_append" if fused else "pa_paged_decode",
+           "split": f"{num_splits} partitions per sequence" if num_splits else "library default (equal ranges)"}
     del inp, out, ws
     return res
 
@@ -586,9 +587,11 @@ def main():
     if args.only_c5:
         w5 = wl.make_c5()
         plain = run_decode_config(w5, timer, stream, args.steps, args.warmup, False, 5)
+        split16 = run_decode_config(w5, timer, stream, args.steps, args.warmup, False, 5, num_splits=16)
         shared = run_prefix_decode(w5, timer, stream, args.steps, args.warmup, 5)
         print(json.dumps({"mode": "only-c5", "workload": "C5 decode", "pa_paged_decode": plain,
-                          "pa_paged_decode_prefix": shared, "steps": args.steps}), flush=True)
+                          "pa_paged_decode_split16": split16, "pa_paged_decode_prefix": shared,
+                          "steps": args.steps}), flush=True)
         copy_calibration(args, stream)
         return
     if args.only_layer:
@@ -643,6 +646,9 @@ def main():
             c5["logical_gbps"] = round(logical / (c5["us_per_layer_step"] * 1e-6) / 1e9, 1)
             extra["C5"] = c5
             log(f"[bench] C5 {c5['us_per_layer_step']} us")
+            # the configuration's stated split: 16 partitions per sequence, merged with log-sum-exp
+            extra["C5_split16"] = run_decode_config(w5, timer, stream, n, nw, False, 5, num_splits=16)
+            log(f"[bench] C5 with 16 partitions per sequence {extra['C5_split16']['us_per_layer_step']} us")
             extra["C5_prefix"] = run_prefix_decode(w5, timer, stream, n, nw, 5)
             log(f"[bench] C5 shared-prefix decode {extra['C5_prefix']['us_per_layer_step']} us")
             extra["C3"] = run_c3(timer, stream, n, args.warmup, 3)

@@ -29,7 +29,7 @@ extern "C" {
 #endif
 
 #define PA_API_VERSION_MAJOR 1
-#define PA_API_VERSION_MINOR 0
+#define PA_API_VERSION_MINOR 1
 
 /* Status codes. Mirrors the integer-error-to-exception mapping of the reference HAL
  * (src/MLFramework/HAL/CUDA/CudaError.cs, CudaException.CheckError used at CudaDevice.cs:15-21). */
@@ -92,6 +92,14 @@ typedef struct pa_config {
                                workgroup (bf16/int8) or 256-token partitions (fp32). Otherwise a
                                multiple of 64 in [64, 4096] (bf16/int8) or 256/512 (fp32).      */
     uint32_t flags;         /* PA_FLAG_*                                                        */
+    int32_t num_splits;     /* bf16/int8 decode: 0 = split by partition_size (above); P in
+                               [1, 256] = every sequence's context is cut into P partitions of
+                               whole blocks (ceil(blocks / P) each, fewer when the sequence has
+                               fewer blocks), each streamed by its own worker per KV head and
+                               merged with a log-sum-exp reduction -- the per-sequence split-K of
+                               DecodeOrchestrator-style long-context decode. Requires
+                               partition_size == 0; must be 0 for fp32 caches; the shared-prefix
+                               decode ignores it.                                               */
 } pa_config;
 
 typedef struct pa_device pa_device;
@@ -203,6 +211,9 @@ pa_status pa_build_slot_mapping(pa_stream* stream, const pa_config* cfg,
  *   (src/MLFramework/Quantization/Operations/QuantizationOperations.cs:188-200).
  *   A block's new tokens may sit anywhere in the call's token list (split by other blocks'
  *   tokens or invalid slots); its segments (maximal runs of them) are applied in call order.
+ *   The int8 append scans the slot list once per touched block (a workgroup per block finds
+ *   whether an earlier token of the call owns its block), so its cost grows as blocks x n_tok:
+ *   prompts above about 16k tokens are best appended in calls of at most that many tokens.
  *   k_scale/v_scale/k_absmax/v_absmax are required for INT8 and ignored otherwise. */
 pa_status pa_kv_append(pa_stream* stream, const pa_config* cfg,
                        const void* k_new, const void* v_new,
@@ -324,7 +335,12 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
  * StandardPagedAttentionKernel.cs:219-255); see PA_FLAG_REFERENCE_LITERAL_MASK.
  *   out: [total_q][num_q_heads][head_dim] fp32, q: [total_q][num_q_heads][head_dim] of
  *   cfg->q_dtype (BF16 or FP32); the cache must be BF16 or INT8.
- *   max_chunk_len: host-side upper bound of the chunk lengths. */
+ *   max_chunk_len: host-side upper bound of the chunk lengths.
+ * Range: every finite cache value is accepted. The P.V product runs on fp16 operands; int8
+ * caches fold log2 of each block's V scale into the softmax exponent, so P times the scale stays
+ * within fp16 for any scale; bf16 caches whose V tiles hold a magnitude above 65504 (fp16's
+ * largest) are detected as the tiles are converted, and the query tiles that read them are
+ * computed again in fp32 (a slower path, taken only for such inputs). */
 pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg, float* out, const void* q,
                              const int32_t* q_start_loc, const int32_t* prefix_lens,
                              const void* k_cache, const void* v_cache,
@@ -382,8 +398,9 @@ pa_status pa_write_block_f32(pa_stream* stream, const pa_config* cfg, void* k_ca
  *      Modules/Linear.cs:81-110). bf16 weights and activations (cfg->q_dtype must be BF16), fp32
  *      accumulation. Batches of at most 64 tokens (decode) run on a weight-streaming MFMA kernel
  *      with the k range split over workgroups (partials added in a fixed order, so results are
- *      deterministic); larger batches, and operands not 16-byte aligned or with the reduced
- *      dimension not a multiple of 128, run on rocBLAS. The first rocBLAS call on a device creates
+ *      deterministic); larger batches, operands not 16-byte aligned, a reduced dimension (hidden
+ *      for Q/K/V, Hq * head_dim for O) not a multiple of 64, and output column counts not a
+ *      multiple of 16 run on rocBLAS. The first rocBLAS call on a device creates
  *      its handle, so make one call of that shape before capturing these into a graph. ---- */
 
 /* Bytes of workspace pa_qkv_project_append needs for n_tok tokens: for n_tok <= 64, the split

@@ -107,6 +107,11 @@ __device__ __forceinline__ void lds_load_runs(u32x4_t rk, u32x4_t rv, const uint
 // The running maximum (log2 units) is raised only when a block's maximum exceeds it by more than
 // this, so unnormalised probabilities stay below 2^12 and the rescale of the accumulators is rare.
 constexpr float kPrefillRescaleLog2 = 12.0f;
+// int8 caches: the exponent of a block's probabilities includes log2 of its V scale, floored here
+// (a zero scale, an invalid block): P then enters the row sum as (P 2^lv) 2^-lv, with 2^-lv <= 2^64
+// keeping the sum finite, and a block whose scale is below 2^-64 contributes P 2^-64 code
+// instead of P scale code (an absolute error below 127 2^-64 of the output).
+constexpr float kMinLog2VScale = -64.0f;
 
 // Waves per workgroup; each computes two (query tile, query head) units.
 constexpr int kPrefillWaves = 4;
@@ -155,6 +160,91 @@ template <int D, int ELT> struct PrefillTile {
     // Memory chunk of block b's V tile stored at position p of the V area (the inverse of vpos).
     __device__ static constexpr int vsrc(int p, int b) { return VRC == 2 ? p ^ b : p; }
 };
+
+// Attention of one unit (query head `head`, queries qrow0 .. qrow0 + nq - 1 of the call, whose
+// first sits at absolute position pos0) over a bf16 cache, in fp32 throughout: lane l holds dims
+// l + 64 j; per key the wave sums q.k across lanes, then updates a running (max, sum, O) with
+// expf. The prefill's fallback when its fp16 V operand cannot hold the cache's values; slow (one
+// key at a time) and exact up to the order of the sums.
+template <int D, bool QF32>
+__device__ void prefill_exact_unit(const PrefillArgs& a, const int32_t* table, int kvh, int head,
+                                                int qrow0, int nq, int pos0, int T, bool causal) {
+    constexpr int DPL = D / 64;
+    const int lane = threadIdx.x & 63;
+    const int Hq = a.num_kv_heads * a.group;
+    const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache);
+    const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache);
+    for (int qi = 0; qi < nq; qi++) {
+        const int64_t qoff = (static_cast<int64_t>(qrow0 + qi) * Hq + head) * D;
+        float qv[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; j++) {
+            const int d = lane + 64 * j;
+            qv[j] = QF32 ? static_cast<const float*>(a.q)[qoff + d]
+                         : pa::bf16_to_f32(static_cast<const uint16_t*>(a.q)[qoff + d]);
+        }
+        const int klim = causal ? min(T, pos0 + qi + 1) : T;
+        float m = -INFINITY, l = 0.0f, o[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; j++) o[j] = 0.0f;
+        for (int t = 0; t < klim; t++) {
+            int id = table[t >> 4];
+            id = id >= 0 && id < a.num_blocks ? id : -1;
+            float s = 0.0f, vv[DPL];
+            const int64_t tile = (static_cast<int64_t>(id >= 0 ? id : 0) * a.num_kv_heads + kvh) * 16 * D;
+#pragma unroll
+            for (int j = 0; j < DPL; j++) {
+                const int d = lane + 64 * j;
+                const float kx = id >= 0 ? pa::bf16_to_f32(kc[tile + (t & 15) * D + d]) : 0.0f;
+                vv[j] = id >= 0 ? pa::bf16_to_f32(vc[tile + d * 16 + (t & 15)]) : 0.0f;
+                s = __builtin_fmaf(qv[j], kx, s);
+            }
+            s = wave_sum(s) * a.scale;
+            const float mn = fmaxf(m, s);
+            const float alpha = expf(m - mn);  // 0 on the first key
+            const float p = expf(s - mn);
+            l = l * alpha + p;
+#pragma unroll
+            for (int j = 0; j < DPL; j++) o[j] = o[j] * alpha + p * vv[j];
+            m = mn;
+        }
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int j = 0; j < DPL; j++) a.out[qoff + lane + 64 * j] = o[j] * inv;
+    }
+}
+
+// The units of round u0 of this workgroup that this wave computes (the kernel's decomposition,
+// rederived from the arguments so that nothing stays live across the stream for this rare path),
+// through prefill_exact_unit.
+template <int D, bool QF32>
+__device__ void prefill_exact_round(const PrefillArgs& a, int u0) {
+    int lid = blockIdx.x;
+    asm volatile("" : "+s"(lid));  // recomputed here, not kept from the kernel's start
+    const int wk = lid >> 3;
+    const int m = wk / a.num_qgroups;
+    const int qg = a.num_qgroups - 1 - (wk - m * a.num_qgroups);
+    const int gi = (lid & 7) + 8 * m;
+    const int seq = gi / a.num_kv_heads, kvh = gi - seq * a.num_kv_heads;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = a.group;
+    const int q0 = a.q_start_loc[seq];
+    const int Lc = a.q_start_loc[seq + 1] - q0;
+    const int P = max(a.prefix_lens[seq], 0);
+    const int i0w = qg * a.qtiles_per_wg * 16;
+    const int T = min(P + Lc, a.max_blocks_per_seq * 16);
+    const bool causal = a.mask_mode == 0 || (a.mask_mode == 1 && P > 0);
+    const int32_t* table = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
+    const int U = a.qtiles_per_wg * G;
+    for (int k = 0; k < 2; k++) {
+        const int u = u0 + 2 * wave + k;
+        if (u >= U) break;
+        const int qtl = u / G;
+        const int i0 = i0w + 16 * qtl;
+        const int nq = max(0, min(16, Lc - i0));
+        if (nq > 0) prefill_exact_unit<D, QF32>(a, table, kvh, kvh * G + (u - qtl * G), q0 + i0, nq, P + i0, T, causal);
+    }
+}
 
 // Work units are (16-query tile, query head) pairs of one KV head. A workgroup takes QT =
 // max(1, kPrefillUnits / G) consecutive query tiles, i.e. QT * G units, kPrefillUnits at a time:
@@ -240,7 +330,15 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
     // Block ids (and int8 scales) of up to KCH key blocks at a time, in LDS.
     constexpr int KCH = D > 64 ? 512 : 1024;  // 3 workgroups per CU at D = 128 fit the LDS with 512
     __shared__ int s_ids[KCH];
-    __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1], s_vsc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1];
+    // int8: K scale, log2 of the V scale (clamped at kMinLog2VScale) and 2^-that
+    __shared__ float s_ksc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1], s_vlg[KV == PA_DTYPE_INT8 ? KCH + 4 : 1],
+        s_vrc[KV == PA_DTYPE_INT8 ? KCH + 4 : 1];
+    // bf16: bit r set when round r (u0 = 8 r; bit 31: round 31 or later) met a V value outside
+    // fp16's range in any wave's conversion
+    __shared__ int s_sat;
+    if constexpr (ELT == 2) {
+        if (tid == 0) s_sat = 0;  // published by the first barrier of the stream
+    }
     const uint32_t tile_lds = lds_address(s_tile);
     // Loads of the pair of blocks jl, jl + 1 (of the current chunk of the table) into slot `slot`.
     // A block past the chunk or with an invalid id gets a zero-sized descriptor and reads as zeros,
@@ -340,8 +438,11 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
 
         // bf16 caches: this wave's V segments of the pair in `slot` (landed: the caller waited for
         // them) become fp16 in place, same positions. Round toward zero: exact for every bf16 value
-        // fp16 represents, larger magnitudes saturate at 65504. The barrier before the pair is
-        // computed publishes the whole fp16 V tiles.
+        // fp16 represents (|v| <= 65280 among bf16 values; subnormal fp16 below 2^-14 keeps an
+        // absolute error under 2^-24); larger magnitudes would saturate at 65504, so the largest
+        // |v| converted is kept in v_big and a round that met one is computed again exactly (see
+        // the end of the round). The barrier before the pair is computed publishes the fp16 tiles.
+        uint64_t v_big = 0;
         auto convert_v = [&](int slot) {
 #pragma unroll
             for (int k = 0; k < NSEG; k++) {
@@ -351,10 +452,14 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                     const uint4 x = *c;
                     const uint32_t w[4] = {x.x, x.y, x.z, x.w};
                     uint32_t o[4];
+                    float mx = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
-                                                                                         __uint_as_float(w[e] & 0xffff0000u)));
+                    for (int e = 0; e < 4; e++) {
+                        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+                        mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
+                        o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+                    }
+                    v_big |= __builtin_amdgcn_ballot_w64(mx >= 65536.0f);  // 65536: the least bf16 above 65504
                     *c = make_uint4(o[0], o[1], o[2], o[3]);
                 }
             }
@@ -408,11 +513,14 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 convert_v(next_slot);
             }
             if constexpr (KV == PA_DTYPE_INT8) {
+                // log2 units plus log2 of the block's V scale: exp2(v - m_run) is then P times the V
+                // scale, at most 2^kPrefillRescaleLog2 whatever the scale, the fp16 P operand
                 const float mult = c2 * s_ksc[jl + pblk];  // 0 for an invalid block
+                const float lvb = s_vlg[jl + pblk];
 #pragma unroll
                 for (int k = 0; k < 2; k++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) v[k][e] *= mult;
+                    for (int e = 0; e < 8; e++) v[k][e] = __builtin_fmaf(v[k][e], mult, lvb);
             }
             if (masked) {  // wave-uniform; only the pairs at the causal edge or past the end
                 const int kq = (lb + pblk) * 16 + ptok;
@@ -455,12 +563,12 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                         for (int i = 0; i < 4; i++) acc[k][t][i] *= ar[i];
                 }
             }
-            // One fp16 P per probability (rounded to nearest, relative error <= 2^-11; P <= 2^12 by
-            // the rescale margin; int8: P times the block's V scale) against V in fp16: bf16 caches'
-            // tiles were converted in LDS when they landed (exact for 2^-14 <= |v| <= 65504), int8
-            // codes are converted here (exact). One PV MFMA per unit and 16-dim tile; bf16 row sums
-            // from one more MFMA against ones, int8 row sums in l_run (before the V scale). The P
-            // of both units first, then each V operand is read right before the MFMAs that use it.
+            // One fp16 P per probability (rounded to nearest, relative error <= 2^-11; at most 2^12
+            // by the rescale margin; int8: P times the block's V scale, by the exponent) against V in
+            // fp16: bf16 caches' tiles were converted in LDS when they landed, int8 codes are
+            // converted here (exact). One PV MFMA per unit and 16-dim tile; bf16 row sums from one
+            // more MFMA against ones, int8 row sums in l_run (P without the V scale). The P of both
+            // units first, then each V operand is read right before the MFMAs that use it.
             f16x8_t pf[2];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
@@ -471,11 +579,10 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                     else p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[k][e], c2, -m_run[k]));
                 }
                 if constexpr (KV == PA_DTYPE_INT8) {
+                    // p holds P times the V scale; the row sum takes P
+                    const float rv = s_vrc[jl + pblk];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) l_run[k] += p[e];
-                    const float vs = s_vsc[jl + pblk];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) p[e] *= vs;
+                    for (int e = 0; e < 8; e++) l_run[k] = __builtin_fmaf(p[e], rv, l_run[k]);
                 }
                 uint32_t w[4];
 #pragma unroll
@@ -534,13 +641,17 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 s_ids[i] = id;
                 if constexpr (KV == PA_DTYPE_INT8) {
                     s_ksc[i] = id >= 0 ? a.k_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
-                    s_vsc[i] = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
+                    const float vsc = id >= 0 ? a.v_scale[static_cast<int64_t>(id) * Hkv + kvh] : 0.0f;
+                    const float lv = fmaxf(__log2f(vsc), kMinLog2VScale);  // log2(0) = -inf -> the floor
+                    s_vlg[i] = lv;
+                    s_vrc[i] = __builtin_amdgcn_exp2f(-lv);
                 }
             }
             if constexpr (KV == PA_DTYPE_INT8) {  // blocks past the end (an odd chunk's partner, a step
-                if (tid < 4) {                      // past the end): scale 0
+                if (tid < 4) {                      // past the end): scale 0, keys masked
                     s_ksc[nkc + tid] = 0.0f;
-                    s_vsc[nkc + tid] = 0.0f;
+                    s_vlg[nkc + tid] = kMinLog2VScale;
+                    s_vrc[nkc + tid] = __builtin_amdgcn_exp2f(-kMinLog2VScale);
                 }
             }
             __syncthreads();
@@ -567,6 +678,9 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 load_slot = load_slot == NSLOT - 1 ? 0 : load_slot + 1;
             }
         }
+        if constexpr (ELT == 2) {
+            if (v_big != 0 && lane == 0) atomicOr(&s_sat, 1 << min(u0 / kPrefillUnits, 31));
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();  // the slots are reused by the next round
 
@@ -592,6 +706,17 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                     for (int t = 0; t < NT; t++) o[16 * t + n] = acc[k][t][i] * inv;
                 }
             }
+        }
+    }
+    if constexpr (ELT == 2) {
+        // A round whose V tiles held |v| > 65504, which the fp16 operand cannot carry, is computed
+        // again in fp32 from the cache by the same waves (their later stores replace the first
+        // ones). Rare: activations that large do not occur in ordinary models. s_sat is final: the
+        // last round's barrier follows every wave's flag.
+        const int sat = s_sat;
+        if (sat != 0) {
+            for (int u0 = 0; u0 < QT * G; u0 += kPrefillUnits)
+                if (sat & (1 << min(u0 / kPrefillUnits, 31))) prefill_exact_round<D, QF32>(a, u0);
         }
     }
 }

@@ -59,6 +59,9 @@ struct DecodeArgs {
     // MFMA kernel: units (range, KV head) the workspace has slots for (2 per unit), computed on the
     // host from the call's shape; the merges follow no slot index at or past 2 * max_units.
     int64_t max_units;
+    // MFMA kernel: > 0 cuts every row (sequence, KV head) into this many partitions of whole
+    // blocks instead of the batch-wide equal ranges (pa_config.num_splits)
+    int32_t num_splits;
 };
 
 // Shared-prefix plan, in device memory: num_groups records {first sequence, members, shared
@@ -290,12 +293,25 @@ __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const Dec
     // (the workspace overwritten in between) is not followed outside the slots.
     if (R0 < 0 || R0 + nbr > total) return;
     const int Hkv = a.num_kv_heads;
+    const int G = a.group;
+    if (a.num_splits > 0) {
+        // Per-sequence split: partitions k < ceil(nbr / c) of c = ceil(nbr / P) blocks, the partial
+        // of partition k in slot 2 ((seq P + k) Hkv + kvh).
+        const int P = a.num_splits;
+        const int c = (nbr + P - 1) / P;
+        const int np = (nbr + c - 1) / c;
+        if (np <= 1) return;  // written whole by the decode kernel
+        if ((static_cast<int64_t>(seq) * P + np) * Hkv > a.max_units) return;
+        merge_partitions<D>(a, seq, kvh, np, [&](int u, int g) {
+            return (2 * ((static_cast<int64_t>(seq) * P + u) * Hkv + kvh)) * G + g;
+        });
+        return;
+    }
     const int64_t C = split_range_blocks(a, total);
     const int64_t w1 = R0 / C, w2 = (R0 + nbr - 1) / C;
     if (w1 == w2) return;  // written whole by the decode kernel
     if ((w2 + 1) * Hkv > a.max_units) return;  // slots the workspace does not have
     const bool starts_inside = R0 != w1 * C;
-    const int G = a.group;
     merge_partitions<D>(a, seq, kvh, static_cast<int>(w2 - w1 + 1), [&](int u, int g) {
         const int64_t unit = (w1 + u) * Hkv + kvh;
         return (2 * unit + (u == 0 && starts_inside ? 1 : 0)) * G + g;

@@ -786,7 +786,11 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     if (total == 0) return;
     const int64_t W = a.split_grid;
     const int64_t C = split_range_blocks(a, total);
-    const int64_t units = (total + C - 1) / C * Hkv;
+    // Per-sequence split (a.num_splits = P > 0, not for the shared-prefix decode): unit u =
+    // ((seq * P) + k) * Hkv + kvh takes partition k of row (seq, kvh), blocks [k c, (k + 1) c) of
+    // the row with c = ceil(blocks / P); its partial goes to slot 2u.
+    const int NSP = SHARED ? 0 : a.num_splits;
+    const int64_t units = NSP > 0 ? static_cast<int64_t>(num_seqs) * NSP * Hkv : (total + C - 1) / C * Hkv;
     // int8 caches: workgroup b runs on XCD b % 8, and consecutive logical workgroups are placed on
     // one XCD, so the KV heads of a range (and neighbouring ranges) are read from one L2 at about
     // the same time (C4 134.8 -> 132.2 us; bf16 caches measured slower with it, 53.3 -> 54.9 us).
@@ -800,6 +804,27 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     int64_t r = u / Hkv;
     int kvh = static_cast<int>(u - r * Hkv);
     int64_t p = r * C, end = min(total, p + C);
+    // Per-sequence split: unit u's block range in the sequence-major list (empty when the row has
+    // fewer than k + 1 partitions' worth of blocks).
+    auto split_range = [&](int64_t su, int64_t& pp, int64_t& ee) {
+        const int64_t sr = su / Hkv;
+        const int sq = static_cast<int>(sr / NSP), k = static_cast<int>(sr - static_cast<int64_t>(sq) * NSP);
+        const int nbr = sh.pref[sq + 1] - sh.pref[sq];
+        const int c = (nbr + NSP - 1) / NSP;
+        pp = sh.pref[sq] + min(nbr, k * c);
+        ee = sh.pref[sq] + min(nbr, (k + 1) * c);
+    };
+    if (NSP > 0) {
+        // the worker's first non-empty unit
+        for (;;) {
+            split_range(u, p, end);
+            if (p < end) break;
+            u += W;
+            if (u >= units) return;
+        }
+        r = u / Hkv;
+        kvh = static_cast<int>(u - r * Hkv);
+    }
     // Sequence holding block position pos (pref[s] <= pos < pref[s + 1]; pos < total): a binary
     // search, so a worker whose range lies far into the batch does not start late behind a chain of
     // dependent LDS reads.
@@ -819,12 +844,18 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     auto next_piece = [&](Piece& g) -> bool {
         if (!mid) {
             if (p >= end) {
-                u += W;
-                if (u >= units) return false;
-                r = u / Hkv;
-                kvh = static_cast<int>(u - r * Hkv);
-                p = r * C;
-                end = min(total, p + C);
+                do {
+                    u += W;
+                    if (u >= units) return false;
+                    r = u / Hkv;
+                    kvh = static_cast<int>(u - r * Hkv);
+                    if (NSP > 0) {
+                        split_range(u, p, end);
+                    } else {
+                        p = r * C;
+                        end = min(total, p + C);
+                    }
+                } while (p >= end);
                 seq = locate(p);
             }
             while (sh.pref[seq + 1] <= p) seq++;
@@ -834,7 +865,7 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
             bool grouped = false;
             if constexpr (SHARED) grouped = (sh.qinfo[seq] >> 24) != 0;
             if (pb0 == 0 && prow_end == nbr) pslot = grouped ? a.row_slot_base + seq * Hkv + kvh : -1;  // whole row
-            else pslot = static_cast<int>(2 * u + (p == r * C ? 0 : 1));
+            else pslot = static_cast<int>(2 * u + (NSP == 0 && p != r * C ? 1 : 0));
         }
         const int b0 = static_cast<int>(p - sh.pref[seq]);
         const int b1 = min(prow_end, b0 + kPieceBlocks);

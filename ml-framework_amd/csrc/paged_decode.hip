@@ -42,6 +42,9 @@ int device_cus() {
 namespace {
 
 using pa::DecodeArgs;
+
+// Largest pa_config.num_splits accepted (partitions per sequence).
+constexpr int kMaxNumSplits = 256;
 using pa::clamp_len;
 using pa::act_at;
 
@@ -50,6 +53,15 @@ using pa::act_at;
 // resident workgroup; otherwise the ranges are `partition_size` tokens (multiple of 64).
 int resolve_part(const pa_config* cfg, std::string* err) {
     const int req = cfg->partition_size;
+    if (cfg->num_splits < 0 || cfg->num_splits > kMaxNumSplits) {
+        *err = "num_splits must be in [0, " + std::to_string(kMaxNumSplits) + "]";
+        return -1;
+    }
+    if (cfg->num_splits > 0 && (cfg->kv_dtype == PA_DTYPE_FP32 || req != 0)) {
+        *err = cfg->kv_dtype == PA_DTYPE_FP32 ? "num_splits applies to bf16 / int8 caches only"
+                                              : "num_splits and partition_size are exclusive";
+        return -1;
+    }
     if (cfg->kv_dtype == PA_DTYPE_FP32) {
         if (req == 0) return 256;
         if (req == 256 || req == 512) return req;
@@ -66,12 +78,13 @@ int resolve_part(const pa_config* cfg, std::string* err) {
 
 // Units (range, KV head) an MFMA launch over (at most) this shape can produce: the bound the
 // workspace is sized for. By default there are at most nr ranges (nr = workers / Hkv, workers <=
-// kMaxDecodeWorkers) of at least 4 blocks each.
-int64_t mfma_max_units(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part) {
+// kMaxDecodeWorkers) of at least 4 blocks each; with num_splits P, P units per (sequence, KV head).
+int64_t mfma_max_units(const pa_config* cfg, int32_t num_seqs, int32_t max_len, int part, int splits) {
     const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
     const int64_t wmax = seqs * ((static_cast<int64_t>(max_len) + 15) / 16);
     const int64_t hkv = cfg->num_kv_heads;
     if (wmax <= 0) return 0;
+    if (splits > 0) return seqs * splits * hkv;
     if (part > 0) return (wmax + part / 16 - 1) / (part / 16) * hkv;
     const int64_t workers = pa::kMaxDecodeWorkers;
     const int64_t nr = workers >= hkv ? workers / hkv : 1;
@@ -88,7 +101,7 @@ size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_l
         return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float);
     }
     const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
-    const int64_t rows = 2 * mfma_max_units(cfg, num_seqs, max_len, part) * (cfg->num_q_heads / cfg->num_kv_heads);
+    const int64_t rows = 2 * mfma_max_units(cfg, num_seqs, max_len, part, cfg->num_splits) * (cfg->num_q_heads / cfg->num_kv_heads);
     return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float) + static_cast<size_t>(seqs + 1) * 4;
 }
 
@@ -231,9 +244,10 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     a.max_parts = max_parts;
     a.part = part;
     a.split_blocks = fp32 ? 0 : part / 16;
+    a.num_splits = fp32 ? 0 : cfg->num_splits;
     a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
     a.scale = pa::resolve_scale(cfg);
-    const int64_t max_units = fp32 ? 0 : mfma_max_units(cfg, num_seqs, max_len, part);
+    const int64_t max_units = fp32 ? 0 : mfma_max_units(cfg, num_seqs, max_len, part, cfg->num_splits);
     a.max_units = max_units;
     if (need > 0) {
         const int64_t rows = fp32 ? static_cast<int64_t>(num_seqs) * cfg->num_q_heads * max_parts : 2 * max_units * G;
@@ -488,7 +502,7 @@ size_t plan_bytes_for(int32_t num_seqs) {
 // Slots of 16 rows: 2 per unit, then one per (row, KV head) of the decode's list (num_seqs +
 // num_groups rows, num_groups <= num_seqs / 2); and a block prefix over the rows.
 int64_t prefix_slots(const pa_config* cfg, int32_t num_seqs, int32_t max_len) {
-    return 2 * mfma_max_units(cfg, num_seqs, max_len, 0) +
+    return 2 * mfma_max_units(cfg, num_seqs, max_len, 0, 0) +
            (static_cast<int64_t>(num_seqs) + num_seqs / 2) * cfg->num_kv_heads;
 }
 size_t prefix_workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_len) {
@@ -608,12 +622,13 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
     a.num_blocks = cfg->num_blocks;
     a.max_context_len = max_len;
     a.max_parts = 1;
-    a.split_blocks = 0;  // equal ranges per worker (partition_size does not apply here)
+    a.split_blocks = 0;  // equal ranges per worker (partition_size and num_splits do not apply here)
+    a.num_splits = 0;
     a.q_bf16 = cfg->q_dtype == PA_DTYPE_BF16;
     a.scale = pa::resolve_scale(cfg);
     a.plan = static_cast<const int32_t*>(plan);
     a.num_groups = num_groups;
-    const int64_t max_units = mfma_max_units(cfg, num_seqs, max_len, 0);
+    const int64_t max_units = mfma_max_units(cfg, num_seqs, max_len, 0, 0);
     a.max_units = max_units;
     const int64_t rows = prefix_slots(cfg, num_seqs, max_len) * pa::kPrefixSlotRows;
     a.row_slot_base = static_cast<int32_t>(2 * max_units);

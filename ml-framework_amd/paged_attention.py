@@ -35,6 +35,9 @@ PA_FLAG_NONE = 0
 PA_FLAG_REFERENCE_LITERAL_MASK = 1
 PA_FLAG_NO_MASK = 2
 
+# bytes of the per-device scratch array of pa_paged_decode_noalloc (PA_NOALLOC_SCRATCH_BYTES)
+PA_NOALLOC_SCRATCH_BYTES = 32 << 20
+
 PA_MEMCPY_HOST_TO_DEVICE = 1
 PA_MEMCPY_DEVICE_TO_HOST = 2
 PA_MEMCPY_DEVICE_TO_DEVICE = 3
@@ -75,6 +78,7 @@ class PaConfig(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("partition_size", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
+        ("num_splits", ctypes.c_int32),
     ]
 
 
@@ -89,9 +93,9 @@ class PaDeviceProps(ctypes.Structure):
 
 
 def make_config(*, num_q_heads, num_kv_heads, head_dim, kv_dtype, q_dtype=PA_DTYPE_FP32,
-                num_blocks, block_size=16, scale=-1.0, partition_size=0, flags=0) -> PaConfig:
+                num_blocks, block_size=16, scale=-1.0, partition_size=0, flags=0, num_splits=0) -> PaConfig:
     return PaConfig(block_size, num_q_heads, num_kv_heads, head_dim, kv_dtype, q_dtype,
-                    num_blocks, scale, partition_size, flags)
+                    num_blocks, scale, partition_size, flags, num_splits)
 
 
 class PagedAttentionError(RuntimeError):

@@ -30,7 +30,7 @@ def test_version_and_status_strings():
     lib = pa.load_library()
     major, minor = ctypes.c_int32(), ctypes.c_int32()
     assert lib.pa_get_version(ctypes.byref(major), ctypes.byref(minor)) == 0
-    assert (major.value, minor.value) == (1, 0)
+    assert (major.value, minor.value) == (1, 1)
     for code, name in [(0, b"PA_SUCCESS"), (1, b"PA_ERROR_INVALID_ARGUMENT"), (2, b"PA_ERROR_INVALID_CONFIG"),
                        (3, b"PA_ERROR_OUT_OF_MEMORY"), (4, b"PA_ERROR_HIP"), (5, b"PA_ERROR_UNSUPPORTED"),
                        (6, b"PA_ERROR_WORKSPACE_TOO_SMALL"), (7, b"PA_ERROR_NO_DEVICE")]:
@@ -127,6 +127,14 @@ def test_workspace_size():
     assert e.value.status == pa.PA_ERROR_UNSUPPORTED
     with pytest.raises(pa.PagedAttentionError):
         pa.decode_workspace_size(cfg(kv_dtype=0, partition_size=1024), 4, 256)
+    # per-sequence split P: P units per (sequence, KV head), 2 slots each
+    assert pa.decode_workspace_size(cfg(num_splits=16), 8, 32768) == 2 * 8 * 16 * 8 * 4 * 130 * 4 + 9 * 4
+    assert pa.decode_workspace_size(cfg(num_splits=1), 3, 100) == 2 * 3 * 8 * 4 * 130 * 4 + 4 * 4
+    for bad in (dict(num_splits=-1), dict(num_splits=257), dict(num_splits=4, partition_size=512),
+                dict(num_splits=4, kv_dtype=0)):
+        with pytest.raises(pa.PagedAttentionError) as e:
+            pa.decode_workspace_size(cfg(**bad), 4, 256)
+        assert e.value.status == pa.PA_ERROR_UNSUPPORTED, bad
 
 
 def test_last_error_is_per_call():

@@ -35,9 +35,9 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def run_decode(w, seed, stream, partition_size=0, n_threads=NTHREADS):
+def run_decode(w, seed, stream, partition_size=0, n_threads=NTHREADS, num_splits=0):
     inp = wl.numpy_inputs(w, seed)
-    cfg = config_for(w, partition_size=partition_size)
+    cfg = config_for(w, partition_size=partition_size, num_splits=num_splits)
     if w.kv_dtype == 2:
         host, g = build_int8_caches(w, inp, stream)
         kc, vc, ks, vs = g["kc"], g["vc"], g["ks"], g["vs"]
@@ -303,6 +303,35 @@ def test_append_int8_out_of_order_bit_exact(stream, D, q_dtype):
     step(slots, [0.25, 1.0, 8.0])
 
 
+@pytest.mark.parametrize("old_scale,new_amax", [(0.5, 127.0), (0.0078125, 3.0), (0.2618793547153473, 95.5709228515625),
+                                               (1.7, 1e4)])
+def test_append_int8_requantisation_all_codes(stream, old_scale, new_amax):
+    """A resident tile holding every code -128..127, then a growth event: the GPU's requantised
+    codes, scales and absmax equal the oracle's bit for bit (the oracle's rule is pinned code by
+    code against the quantiser primitives in test_oracle.py)."""
+    nb, hkv, D, row = 2, 2, 64, 5
+    cfg = pa.make_config(num_q_heads=hkv, num_kv_heads=hkv, head_dim=D, kv_dtype=2, q_dtype=0, num_blocks=nb)
+    codes = (np.arange(16 * D) % 256 - 128).astype(np.int8)
+    kc = np.zeros((nb, hkv, 16, D), np.int8)
+    for h in range(hkv):
+        kc[1, h] = np.roll(codes, 37 * h).reshape(16, D)
+    os_ = np.float32(old_scale)
+    host = dict(kc=kc, vc=kc.copy(), ks=np.full((nb, hkv), os_, np.float32), vs=np.full((nb, hkv), os_, np.float32),
+                ka=np.full((nb, hkv), os_ * np.float32(127), np.float32),
+                va=np.full((nb, hkv), os_ * np.float32(127), np.float32))
+    dev = {n: to_gpu(a) for n, a in host.items()}
+    x = np.zeros((1, hkv, D), np.float32)
+    x[0, :, 0] = np.float32(new_amax)
+    x[0, :, 1] = -np.float32(new_amax) / np.float32(3)
+    slots = np.array([16 + row], np.int64)
+    orc.kv_append(cfg, x, x, slots, host["kc"], host["vc"], host["ks"], host["vs"], host["ka"], host["va"])
+    pa.kv_append(stream, cfg, to_gpu(x), to_gpu(x), to_gpu(slots), 1, dev["kc"], dev["vc"], dev["ks"], dev["vs"],
+                 dev["ka"], dev["va"])
+    _sync()
+    for n, a in host.items():
+        np.testing.assert_array_equal(to_np(dev[n]), a, err_msg=n)
+
+
 # ---- decode -----------------------------------------------------------------------------------------
 def test_decode_c1_fp32(stream):
     """C1, the CPU-parity configuration (fp32 cache and query, VALU kernel), at the fp32 bar."""
@@ -366,6 +395,20 @@ def test_decode_long_segments(stream, kv_dtype, part):
     check_close(got, ref, **tol_for(kv_dtype), what=f"long segments kv={kv_dtype} part={part}")
 
 
+@pytest.mark.parametrize("nsp", [1, 3, 16, 200])
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [(1, 1, 32, 8, 128), (2, 0, 16, 4, 128), (1, 0, 8, 8, 64)])
+def test_decode_num_splits(stream, nsp, kv_dtype, q_dtype, Hq, Hkv, D):
+    """pa_config.num_splits = P: every sequence cut into P partitions of whole blocks (fewer when it
+    has fewer blocks), one worker per (partition, KV head), merged per row; edge lengths and long
+    rows, P above and below the block counts."""
+    lens = EDGE_LENS + [5000, 40000, 16 * 200, 16 * 200 + 1]
+    w = wl.make_small(300 + nsp + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D, kv_dtype=kv_dtype,
+                      q_dtype=q_dtype)
+    got, ref = run_decode(w, 61, stream, num_splits=nsp)
+    check_close(got, ref, **tol_for(kv_dtype), what=f"num_splits={nsp} kv={kv_dtype} D={D}")
+    assert np.all(got[0] == 0.0)
+
+
 def test_decode_invalid_block_ids_read_as_zero(stream):
     w = wl.make_small(9, num_seqs=4, lens=[40, 300, 700, 33], Hq=16, Hkv=4, D=128, kv_dtype=1, q_dtype=1)
     w.block_tables[1, 3] = -1
@@ -384,16 +427,18 @@ LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000]
 
 
 @pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,part,lens", [
+    (1, 1, 32, 8, 128, -16, APPEND_LENS), (2, 0, 32, 8, 128, -5, APPEND_LENS),
     (1, 1, 32, 8, 128, 0, APPEND_LENS), (1, 0, 16, 4, 64, 512, APPEND_LENS), (2, 0, 32, 8, 128, 0, APPEND_LENS),
     (2, 1, 8, 2, 256, 512, APPEND_LENS), (0, 0, 8, 8, 64, 256, APPEND_LENS), (0, 1, 16, 4, 128, 512, APPEND_LENS),
     (1, 1, 16, 4, 128, 256, APPEND_LENS), (1, 1, 8, 2, 128, 4096, LONG_LENS), (2, 1, 8, 2, 128, 0, LONG_LENS),
-], ids=["bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
+], ids=["bf16-split16", "int8-split5", "bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
         "int8-long"])
 def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part, lens):
     w = wl.make_small(70 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
                       kv_dtype=kv_dtype, q_dtype=q_dtype)
     inp = wl.numpy_inputs(w, 77)
-    cfg = config_for(w, partition_size=part)
+    # part < 0: num_splits = -part partitions per sequence instead of a partition length
+    cfg = config_for(w, partition_size=max(part, 0), num_splits=max(-part, 0))
     S = w.num_seqs
     rng = np.random.default_rng(78)
     k_new = rng.standard_normal((S, Hkv, D), dtype=np.float32)

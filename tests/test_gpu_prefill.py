@@ -30,7 +30,8 @@ def stream():
     s.device.close()
 
 
-def run_prefill(stream, *, prefix, chunk, Hq, Hkv, D, kv_dtype, q_dtype, flags=0, seed=0, table_edit=None):
+def run_prefill(stream, *, prefix, chunk, Hq, Hkv, D, kv_dtype, q_dtype, flags=0, seed=0, table_edit=None,
+                input_edit=None):
     import torch
 
     prefix = np.asarray(prefix, np.int32)
@@ -41,6 +42,8 @@ def run_prefill(stream, *, prefix, chunk, Hq, Hkv, D, kv_dtype, q_dtype, flags=0
     if table_edit is not None:
         table_edit(w)
     inp = wl.numpy_inputs(w, 400 + seed)
+    if input_edit is not None:
+        input_edit(w, inp)
     cfg = config_for(w, flags=flags)
     if kv_dtype == 2:
         host, g = build_int8_caches(w, inp, stream)
@@ -124,3 +127,48 @@ def test_prefill_rows_match_decode(stream):
                     to_gpu(w.block_tables), to_gpu(totals), 3, w.max_blocks, int(totals.max()), ws, wsb)
     torch.cuda.synchronize()
     check_close(got[q_start[1:] - 1], to_np(out), **tol_for(1), what="last prefill row vs decode")
+
+
+def _bf16_outliers(w, inp):
+    """About 0.3 % of the bf16 V cache set to +-[65536, 1e5): magnitudes fp16 cannot hold."""
+    rng = np.random.default_rng(77)
+    v = inp["v_cache"].view(np.uint16).reshape(-1)
+    idx = rng.choice(v.size, size=max(8, v.size // 300), replace=False)
+    mag = rng.uniform(65536.0, 1e5, size=idx.size).astype(np.float32)
+    sign = np.where(rng.random(idx.size) < 0.5, -1.0, 1.0).astype(np.float32)
+    v[idx] = orc.bf16_from_f32(mag * sign)
+
+
+def _scale_v(factor):
+    """The whole V cache multiplied by a power of two: every bf16 value and every int8 code stays
+    the same up to the exact factor (int8: the scale absmax / 127 takes the factor exactly, the
+    codes do not change), so the exact attention output is the unscaled one times the factor."""
+    def edit(w, inp):
+        if w.kv_dtype == 2:
+            inp["v_src"] *= np.float32(factor)
+        else:
+            v = orc.f32_from_bf16(inp["v_cache"]) * np.float32(factor)
+            inp["v_cache"] = orc.bf16_from_f32(v)
+    edit.factor = factor
+    return edit
+
+
+@pytest.mark.parametrize("flags", [0, pa.PA_FLAG_REFERENCE_LITERAL_MASK, pa.PA_FLAG_NO_MASK])
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,edit", [
+    (1, 1, 32, 8, 128, _bf16_outliers), (1, 0, 8, 2, 64, _bf16_outliers),
+    (1, 1, 32, 8, 128, _scale_v(2.0 ** 16)), (2, 1, 16, 4, 128, _scale_v(4096.0)), (2, 0, 8, 8, 64, _scale_v(4096.0)),
+], ids=["bf16-outliers", "bf16-outliers-d64", "bf16-x65536", "int8-x4096", "int8-x4096-d64"])
+def test_prefill_values_beyond_fp16_range(stream, flags, kv_dtype, q_dtype, Hq, Hkv, D, edit):
+    """V magnitudes past fp16's 65504.
+    bf16 outliers: 0.3 % of V entries at +-[65536, 1e5) among N(0,1) values, at the unchanged bar
+    (an output dim mixes only that dim's V values, so the outliers' dims are held to 1e-2 of their
+    size). Scaled V (bf16 x 2^16: |V| up to ~3e5; int8 x 4096: block V scales ~100, P times the scale
+    far past fp16): attention is linear in V and the factor is exact, so outputs divided by the
+    factor are held to the unit-scale bar -- the bar the errors of fp16 / bf16 probabilities scale
+    with."""
+    got, ref = run_prefill(stream, prefix=[0, 17, 300, 40], chunk=[40, 33, 64, 1], Hq=Hq, Hkv=Hkv, D=D,
+                           kv_dtype=kv_dtype, q_dtype=q_dtype, flags=flags, seed=11 + D + kv_dtype,
+                           input_edit=edit)
+    f = getattr(edit, "factor", 1.0)
+    assert np.abs(ref).max() > 1000.0, "the case must reach large outputs"
+    check_close(got / f, ref / f, **tol_for(kv_dtype), what=f"large V kv={kv_dtype} D={D} flags={flags} x{f}")

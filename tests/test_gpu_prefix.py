@@ -231,8 +231,9 @@ def test_prefix_decode_graph_replay_matches_eager():
 def test_c5_full_size_vs_oracle(stream):
     """Full C5 (8 sequences of 16-32k tokens, 512 shared blocks): pa_paged_decode with the default
     split and pa_paged_decode_prefix, the two calls bench.py times, each against the oracle's
-    whole-context decode; a 64-token split (about 500 partials per row: the merge's multi-round
-    path) against the default split."""
+    whole-context decode; the configuration's stated split (num_splits = 16 partitions per sequence
+    with the log-sum-exp merge) against the oracle as well; a 64-token split (about 500 partials per
+    row: the merge's multi-round path) against the default split."""
     import torch
 
     w = wl.make_c5()
@@ -249,8 +250,8 @@ def test_c5_full_size_vs_oracle(stream):
     tables, lens = to_gpu(w.block_tables), to_gpu(w.context_lens)
     mcl = w.max_context_len
     outs = {}
-    for name, part in (("default", 0), ("p64", 64)):
-        cfg = config_for(w, partition_size=part)
+    for name, part, nsp in (("default", 0, 0), ("p64", 64, 0), ("split16", 0, 16)):
+        cfg = config_for(w, partition_size=part, num_splits=nsp)
         wsb = pa.decode_workspace_size(cfg, S, mcl)
         ws = empty_gpu((wsb,), np.uint8)
         out = empty_gpu((S, Hq, D), np.float32)
@@ -275,4 +276,5 @@ def test_c5_full_size_vs_oracle(stream):
                            w.block_tables, w.context_lens, n_threads=NTHREADS)
     check_close(outs["default"], ref, **tol_for(1), what="C5 pa_paged_decode vs oracle")
     check_close(outs["prefix"], ref, **tol_for(1), what="C5 pa_paged_decode_prefix vs oracle")
+    check_close(outs["split16"], ref, **tol_for(1), what="C5 with 16 partitions per sequence vs oracle")
     check_close(outs["p64"], outs["default"], **tol_for(1), what="C5 64-token split vs default")

@@ -42,7 +42,7 @@ def test_qkv_project_append(kv_dtype, hkv, hq, d, hidden, n_tok):
     cols = (hq + 2 * hkv) * d
     x = orc.bf16_from_f32(rng.standard_normal((n_tok, hidden), dtype=np.float32))
     w = orc.bf16_from_f32((rng.standard_normal((cols, hidden), dtype=np.float32) / np.sqrt(hidden)).astype(np.float32))
-    # one token per block (int8 appends need a block's tokens consecutive in the call)
+    # one token per block, at a random row of it
     slots = (rng.permutation(nb)[:n_tok] * 16 + rng.integers(0, 16, n_tok)).astype(np.int64)
     if n_tok > 3:
         slots[3] = -1  # skipped

@@ -356,6 +356,81 @@ def test_append_int8_policy_invariants():
     assert ka[2, 0] == np.abs(z[0, 0]).max()
 
 
+def _requant_case(old_scale, new_amax, H=2, D=64, row=5):
+    """One int8 block whose resident tile holds every code -128..127 (each 4 times per head) under
+    old_scale, then an append at `row` whose max |x| is new_amax > the block's absmax: the
+    state before and after, through the oracle's append."""
+    nb = 2
+    cfg = pa.make_config(num_q_heads=H, num_kv_heads=H, head_dim=D, kv_dtype=2, num_blocks=nb)
+    codes = (np.arange(16 * D) % 256 - 128).astype(np.int8)
+    kc = np.zeros((nb, H, 16, D), np.int8)
+    for h in range(H):
+        kc[1, h] = np.roll(codes, 37 * h).reshape(16, D)
+    vc = kc.copy()
+    ks = np.full((nb, H), f32(old_scale), f32)
+    ka = np.full((nb, H), f32(old_scale) * f32(127), f32)
+    vs, va = ks.copy(), ka.copy()
+    x = np.zeros((1, H, D), f32)
+    x[0, :, 0] = f32(new_amax)
+    x[0, :, 1] = -f32(new_amax) / f32(3)
+    before = kc.copy()
+    orc.kv_append(cfg, x, x, np.array([16 + row], np.int64), kc, vc, ks, vs, ka, va)
+    return before, kc, vc, ks, ka, x
+
+
+@pytest.mark.parametrize("old_scale,new_amax,separates", [
+    (0.5, 127.0, False),        # new scale exactly 2x: every odd code lands on a tie (k + 0.5)
+    (0.25, 127.0, False),       # 4x: ties at odd multiples of 2
+    (1.0, 190.5, False),        # 1.5x: mixed fractions
+    (0.0078125, 3.0, False),    # tiny scales, large ratio: most codes collapse to 0 / +-1
+    (0.3, 38.1 + 1e-3, False),  # ratio just above 1: codes almost unchanged, fp32 rounding decides
+    (1.7, 1e4, False),          # huge growth: every resident code becomes 0 or +-1
+    # a pair (found by search) where the fp32 rounding of the ratio moves code -125 to -43
+    # instead of -44: the case that separates the shortcut q * (old / new)
+    (0.2618793547153473, 95.5709228515625, True),
+])
+def test_append_int8_requantisation_exact(old_scale, new_amax, separates):
+    """After a growth event every resident code equals QuantizeSymmetric(Dequantize(code, old),
+    new) with the KAT-pinned primitives (QuantizationOperations.cs:83-88, 188-200): all 256 codes,
+    ties included, and also the exact-rational rounding rule on the fp32 quotient. The ratio
+    shortcut q * (old / new) is shown to differ on these inputs, so the test tells them apart."""
+    H, D, row = 2, 64, 5
+    old_scale = float(f32(old_scale))
+    before, kc, vc, ks, ka, x = _requant_case(old_scale, new_amax, H, D, row)
+    new_scale = f32(f32(new_amax) / f32(127))
+    assert ks[1, 0] == new_scale and ka[1, 0] == f32(new_amax)
+    shortcut_differs = False
+    ratio = f32(f32(old_scale) / new_scale)
+    for h in range(H):
+        for r in range(16):
+            for d in range(D):
+                c = int(before[1, h, r, d])
+                got = int(kc[1, h, r, d])
+                if r == row:
+                    assert got == L.orc_quantize_symmetric(float(x[0, h, d]), float(new_scale))
+                    continue
+                deq = L.orc_dequantize(c, float(old_scale))
+                assert deq == f32(c) * f32(old_scale)
+                expect = L.orc_quantize_symmetric(deq, float(new_scale))
+                assert got == expect, (h, r, d, c, got, expect)
+                # the rounding rule on the exact fp32 quotient, by rational arithmetic
+                quot = Fraction(float(f32(f32(deq) / new_scale)))
+                assert got == max(-128, min(127, _nearest_away(quot)))
+                if L.orc_quantize_symmetric(float(f32(c) * ratio), 1.0) != expect:
+                    shortcut_differs = True
+    assert shortcut_differs == separates
+    # V: the tile is dim-major; resident element (row r, dim d) sits at d * 16 + r
+    for h in range(H):
+        bt, vt = before[1, h].reshape(-1), vc[1, h].reshape(-1)
+        for r in range(16):
+            if r == row:
+                continue
+            for d in range(0, D, 7):
+                c = int(bt[d * 16 + r])
+                assert int(vt[d * 16 + r]) == L.orc_quantize_symmetric(L.orc_dequantize(c, float(old_scale)),
+                                                                       float(new_scale))
+
+
 def _segments(slots, nb):
     """Maximal runs of consecutive valid slots that lie in one block: (start, end) pairs."""
     segs, i, n = [], 0, len(slots)

@@ -12,7 +12,7 @@ import pytest
 import paged_attention as pa
 import pa_oracle as orc
 import workloads as wl
-from helpers import check_close, config_for, empty_gpu, to_gpu, to_np, tol_for
+from helpers import build_int8_caches, check_close, config_for, empty_gpu, to_gpu, to_np, tol_for
 
 pytestmark = pytest.mark.gpu
 NTHREADS = min(16, os.cpu_count() or 1)
@@ -41,8 +41,13 @@ def _run_both(stream, w, inp):
 
     cfg = config_for(w)
     S, mcl = w.num_seqs, w.max_context_len
-    args = (to_gpu(inp["q"]), to_gpu(inp["k_cache"]), to_gpu(inp["v_cache"]), None, None, to_gpu(w.block_tables),
-            to_gpu(w.context_lens), S, w.max_blocks, mcl)
+    if w.kv_dtype == 2:  # int8: the pool quantised by the GPU append (checked against the oracle's)
+        host, g = build_int8_caches(w, inp, stream)
+        caches = (g["kc"], g["vc"], g["ks"], g["vs"])
+    else:
+        host = dict(k_cache=inp["k_cache"], v_cache=inp["v_cache"], k_scale=None, v_scale=None)
+        caches = (to_gpu(inp["k_cache"]), to_gpu(inp["v_cache"]), None, None)
+    args = (to_gpu(inp["q"]), *caches, to_gpu(w.block_tables), to_gpu(w.context_lens), S, w.max_blocks, mcl)
     wsb = pa.decode_workspace_size(cfg, S, mcl)
     ws = empty_gpu((max(wsb, 1),), np.uint8)
     ref_out = empty_gpu((S, w.num_q_heads, w.head_dim), np.float32)
@@ -53,12 +58,12 @@ def _run_both(stream, w, inp):
     pa.paged_decode_noalloc(stream, cfg, out, *args)
     stream.synchronize()
     got, want = to_np(out).copy(), to_np(ref_out).copy()
-    ref = orc.paged_decode(cfg, inp["q"], inp["k_cache"], inp["v_cache"], None, None, w.block_tables, w.context_lens,
-                           n_threads=NTHREADS)
+    ref = orc.paged_decode(cfg, inp["q"], host["k_cache"], host["v_cache"], host["k_scale"], host["v_scale"],
+                           w.block_tables, w.context_lens, n_threads=NTHREADS)
     return got, want, ref, wsb
 
 
-@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [(1, 1, 32, 8, 128), (0, 0, 8, 2, 64)])
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [(1, 1, 32, 8, 128), (0, 0, 8, 2, 64), (2, 0, 32, 8, 128)])
 def test_noalloc_decode_matches_workspace_decode_twice(stream, kv_dtype, q_dtype, Hq, Hkv, D):
     rng = np.random.default_rng(40 + kv_dtype)
     big = rng.integers(1, 3000, size=40).tolist() + [4096, 0, 1]
@@ -69,6 +74,19 @@ def test_noalloc_decode_matches_workspace_decode_twice(stream, kv_dtype, q_dtype
         assert wsb > 0, "the case must use a split-K workspace"
         np.testing.assert_array_equal(got, want, err_msg=f"call {i}: noalloc output differs from pa_paged_decode")
         check_close(got, ref, **tol_for(kv_dtype), what=f"call {i} vs oracle")
+
+
+def test_noalloc_chunked_call_matches_workspace_decode_twice(stream):
+    """More sequences than one persistent launch takes (2047): the call runs in chunks of
+    sequences that reuse the same scratch one after another; twice in a row, the second smaller."""
+    rng = np.random.default_rng(47)
+    for i, n in enumerate((2300, 2100)):
+        lens = rng.integers(1, 48, size=n).tolist()
+        w, inp = _case(700 + i, lens, 8, 2, 64, 1, 1)
+        got, want, ref, wsb = _run_both(stream, w, inp)
+        assert 0 < wsb <= pa.PA_NOALLOC_SCRATCH_BYTES
+        np.testing.assert_array_equal(got, want, err_msg=f"call {i}: noalloc output differs from pa_paged_decode")
+        check_close(got, ref, **tol_for(1), what=f"chunked call {i} vs oracle")
 
 
 def test_noalloc_refuses_a_shape_beyond_its_scratch(stream):
