@@ -251,8 +251,9 @@ pa_status pa_paged_decode(pa_stream* stream, const pa_config* cfg, float* out, c
  * (k_new/v_new [num_seqs][num_kv_heads][head_dim] of cfg->q_dtype) into the cache, then runs
  * pa_paged_decode. Cache bytes, int8 scales and absmax after the call are exactly those of
  * pa_kv_append with slot_mapping[s] = block_tables[s][(T-1)/16] * 16 + (T-1) % 16 followed by
- * pa_paged_decode; for bf16 caches both happen in one kernel (the wave that owns a sequence's
- * last block patches the new token into its registers and the cache), for int8 caches the
+ * pa_paged_decode; for bf16 caches both happen in one kernel (the rows stream their first T - 1
+ * cached tokens and the new token joins each row's softmax from k_new / v_new, truncated to bf16 as
+ * the cache stores it, while the wave that ends the row writes it into the cache), for int8 caches the
  * quantising append is a launch of its own ahead of the decode, and for fp32 caches a plain
  * copy kernel. No reference counterpart: the reference appends (PagedAttentionLayer.UpdateKVCache,
  * Layers/PagedAttentionLayer.cs:244-296) and decodes (DecodeOrchestrator.ComputeDecodeAttention,

@@ -413,45 +413,9 @@ __device__ __forceinline__ int k_dim0(int sl, int q4) {
     return KV == PA_DTYPE_INT8 ? (D / 4) * q4 + 8 * sl : 32 * sl + 8 * q4;
 }
 
-// ---- fused append: the new token (row r of the sequence's last block) enters the owning wave's
-// registers and the cache. Values and cache bytes are those of pa_kv_append for that one token.
+// Element i of an activation array (the fused append's new K/V): fp32, or bf16 widened exactly.
 __device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
     return f32 ? static_cast<const float*>(p)[i] : pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
-
-// The new token's K values are at s_new[0, D) and its V values at s_new[D, 2D) (LDS, fp32 holding
-// the activation values). The owning wave patches row r of the tile it holds in registers and
-// writes the same bytes to the cache.
-template <int D>
-__device__ __forceinline__ void append_bf16_regs(const DecodeArgs& a, int64_t tile, const float* s_new, int r,
-                                                 int q4, int n, uint4 (&kr)[D / 32], uint2 (&vr)[D / 16]) {
-    constexpr int NSLAB = D / 32, NT = D / 16;
-    uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache));
-    uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache));
-    if (n == r) {  // K row r: dims 32s + 8q4 .. +8 of this lane
-#pragma unroll
-        for (int sl = 0; sl < NSLAB; sl++) {
-            const int d0 = k_dim0<D, PA_DTYPE_BF16>(sl, q4);
-            const float* x = s_new + d0;
-            const uint4 v = make_uint4(pack_bf16_trunc(x[0], x[1]), pack_bf16_trunc(x[2], x[3]),
-                                       pack_bf16_trunc(x[4], x[5]), pack_bf16_trunc(x[6], x[7]));
-            kr[sl] = v;
-            *reinterpret_cast<uint4*>(kc + tile + r * D + d0) = v;
-        }
-    }
-    if (q4 == (r >> 2)) {  // V column r: element r & 3 of this lane's 4-token run, dims 16t + n
-        const int e = r & 3;
-        const uint32_t sh = (e & 1) * 16;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int d = 16 * t + n;
-            const uint32_t b = __float_as_uint(s_new[D + d]) >> 16;
-            const uint32_t mask = ~(0xffffu << sh);
-            if (e < 2) vr[t].x = (vr[t].x & mask) | (b << sh);
-            else vr[t].y = (vr[t].y & mask) | (b << sh);
-            vc[tile + d * 16 + r] = static_cast<uint16_t>(b);
-        }
-    }
 }
 
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).

@@ -15,11 +15,19 @@
 //
 // A portion is streamed in pieces of at most 64 blocks (lane j holds the id of the piece's block
 // j); the running (max, sum, O) carry over from piece to piece and are written when the portion
-// ends. Block ids are loaded two pieces ahead. Kernels without the fused append (and with bf16
-// queries, head_dim <= 128) also carry the pipeline across pieces: a piece issues the next one's
-// Q and scales at its start and its first two blocks in its last two iterations, so a piece or
-// row boundary does not drain the blocks in flight. The others start a piece with its own loads
-// (one memory round trip).
+// ends. Block ids are loaded two pieces ahead. Kernels with bf16 queries and head_dim <= 128 also
+// carry the pipeline across pieces: a piece issues the next one's Q and scales at its start and
+// its first two blocks in its last two iterations, so a piece or row boundary does not drain the
+// blocks in flight. The others start a piece with its own loads (one memory round trip).
+//
+// Fused append (pa_paged_decode_append, bf16 caches): a row streams its first T - 1 cached tokens
+// only; the new token (position T - 1, from k_new / v_new) joins the softmax as one more element at
+// the end of the row portion that holds the row's last streamed block, and that portion's wave
+// writes it into the cache: its K row as is, its V column by rewriting the whole V tile (fetched
+// into LDS when the piece starts, patched there, stored back as full lines -- 2-byte stores at a
+// 32-byte stride, one per dim, cost the step about 3 us of partial-line writes). No block is
+// patched in registers, so the fused kernel streams with the same loop (and carry) as the plain
+// decode.
 //
 // Per block: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads padded
 // to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
@@ -74,11 +82,12 @@ __host__ __device__ constexpr int decode_buffers(int kv) { return kv == PA_DTYPE
 
 // Ids of a piece's blocks: lane j holds block b0 + j (-1 beyond the piece). Ids are range-checked
 // where they are used (valid_bid): a check here would make the wave wait for the table load at the
-// point of issue instead of when the id is needed.
-__device__ __forceinline__ int piece_ids(const DecodeArgs& a, const Piece& g, int lane) {
+// point of issue instead of when the id is needed. With `extra`, lane b1 - b0 holds the id of
+// block b1 as well.
+__device__ __forceinline__ int piece_ids(const DecodeArgs& a, const Piece& g, int lane, bool extra = false) {
     const int b = g.b0 + lane;
     int id = -1;
-    if (b < g.b1) id = a.block_tables[static_cast<int64_t>(g.seq) * a.max_blocks_per_seq + b];
+    if (b < g.b1 || (extra && b == g.b1)) id = a.block_tables[static_cast<int64_t>(g.seq) * a.max_blocks_per_seq + b];
     return id;
 }
 __device__ __forceinline__ int valid_bid(const DecodeArgs& a, int id) { return id < a.num_blocks ? id : -1; }
@@ -132,23 +141,27 @@ __host__ __device__ constexpr int vmcnt_keep() {
     return (N & 15) | 0x7 << 4 | 0xf << 8 | (N >> 4) << 14;
 }
 
-// Carry across pieces (bf16 queries, head_dim <= 128, no fused append): elsewhere the extra
-// registers (the next piece's Q) would spill, so those kernels start every piece with its own loads.
+// Carry across pieces (bf16 queries, head_dim <= 128): elsewhere the extra registers (the next
+// piece's Q) would spill, so those kernels start every piece with its own loads.
 template <int D, int KV, bool QF32, bool APPEND>
 __host__ __device__ constexpr bool decode_carry() {
-    return decode_buffers(KV) == 3 && !QF32 && !APPEND && D <= 128;
+    return decode_buffers(KV) == 3 && !QF32 && D <= 128;
 }
 
-// Fused append: the row's last block is entry j_app of the piece that ends the row (-1: none).
+// Fused append (pa_paged_decode_append, bf16 caches): Piece::T counts the streamed tokens, the
+// new token sits at position T; the piece that ends the portion holding the row's last streamed
+// block appends it.
 template <bool APPEND>
-__device__ __forceinline__ int piece_app(const Piece& g) {
-    if constexpr (!APPEND) return -1;
-    const int nbrow = (g.T + 15) / 16;
-    return g.b1 == nbrow ? nbrow - 1 - g.b0 : -1;
+__device__ __forceinline__ bool piece_owns_new(const Piece& g) {
+    if constexpr (!APPEND) return false;
+    return g.last && g.b1 == (g.T + 15) / 16;
 }
-// List entry consumed by iteration j of a piece: the appended block first (its patch then happens
-// while the pipeline fills), then the others in order.
-__device__ __forceinline__ int piece_entry(int j_app, int j) { return j_app > 0 ? (j == 0 ? j_app : j - 1) : j; }
+// The block ids a piece loads: its own, plus for the owning piece whose new token starts a block
+// (T % 16 == 0) that block's id in lane b1 - b0 (when the piece has fewer than 64 blocks).
+template <bool APPEND>
+__device__ __forceinline__ int piece_ids_of(const DecodeArgs& a, const Piece& g, int lane) {
+    return piece_ids(a, g, lane, piece_owns_new<APPEND>(g) && (g.T & 15) == 0);
+}
 
 // Side loads of piece g (ids: its block ids, lane j = block j): Q, the appended token and, when
 // `scales`, the int8 scales (those need the ids, which may still be in flight).
@@ -190,7 +203,7 @@ __device__ __forceinline__ void load_side(const DecodeArgs& a, const Piece& g, i
         }
     }
     if constexpr (APPEND) {
-        if (piece_app<APPEND>(g) >= 0 && lane * NPL < D) {
+        if (piece_owns_new<APPEND>(g) && lane * NPL < D) {
             const int64_t src = (static_cast<int64_t>(g.seq) * Hkv + g.kvh) * D + lane * NPL;
 #pragma unroll
             for (int w = 0; w < NW; w++) {
@@ -257,11 +270,13 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
 // previous piece, or for a worker's first piece by the worker), and it issues the next piece's
 // side loads at its start and its first two blocks in its last two iterations. prefetch_next() is
 // called once, after the piece's first loads, to start the id loads of the piece after the next.
-// s_new: this wave's LDS staging of the appended token (2 * D floats).
+// s_new: this wave's LDS staging of the appended token (2 * D floats); s_vt: its V tile staging
+// (16 D bf16).
 template <int D, int KV, bool QF32, bool APPEND, bool SHARED, typename Prefetch>
 __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, int my_bid,
                                            PieceSide<D, QF32>& side, PipeBufs<D, KV>& bufs, RowState<D / 16>& st,
-                                           float* s_new, const bool& has_next, const Piece& nxt, const int& nxt_ids,
+                                           float* s_new, uint4* s_vt, const bool& has_next, const Piece& nxt,
+                                           const int& nxt_ids,
                                            PieceSide<D, QF32>& nside, Prefetch&& prefetch_next) {
     using Raw = MfmaRaw<KV>;
     constexpr int NSLAB = D / 32;  // QK MFMAs (k = 32 dims each)
@@ -282,12 +297,11 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     // (without carry), the ids of the piece after the next (prefetch callback) and the next piece's
     // side loads (with carry). Memory returns in order, so the K/V requests go out first; none of the other values is
     // used right after its load (that would stall the wave on the load's latency).
-    // Fused append (bf16 caches; int8 caches are appended by a separate launch first): the wave
-    // that streams the row's last block fetches the new token (lane l: dims l*NPL ..); the token's
-    // raw bits (fp32, or bf16 packed two per word) are decoded only at the patch.
+    // Fused append (bf16 caches; int8 caches are appended by a separate launch first): the piece
+    // that ends the row's owning portion fetches the new token with its side loads (lane l: dims
+    // l*NPL ..); the token's raw bits (fp32, or bf16 packed two per word) are decoded at the end.
     static_assert(!(APPEND && KV == PA_DTYPE_INT8), "int8 caches are appended before the decode");
-    const int j_app = piece_app<APPEND>(g);
-    auto entry = [&](int j) { return piece_entry(j_app, j); };
+    auto entry = [](int j) { return j; };
     auto new_val = [&](const uint32_t (&raw)[NW], int e) -> float {
         if constexpr (QF32) return __uint_as_float(raw[e]);
         else if constexpr (NPL == 1) return __uint_as_float(raw[0] << 16);
@@ -416,40 +430,13 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     float& l_run = st.l_run;
     f32x4_t(&acc)[NT] = st.acc;
 
-    // app: this call may hold the appended block (only the one outside the loop below does).
-    auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j, bool app) {
+    auto compute = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int j) {
         const int e = entry(j);
         const int bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, e));
         float ks = 1.0f, vfac = 1.0f;
         if constexpr (KV == PA_DTYPE_INT8) {
             ks = bid >= 0 ? readlane_f(side.ks, e) : 0.0f;
             vfac = bid >= 0 ? readlane_f(side.vs, e) : 0.0f;
-        }
-        if constexpr (APPEND) {
-            if (app && e == j_app && bid >= 0) {
-                // Stage the new token in this wave's LDS area, then patch the tile.
-                // The empty asm keeps the decoding here: hoisted out of the loop, it would wait
-                // for the token's loads before the first block.
-                uint32_t kw[NW], vw[NW];
-#pragma unroll
-                for (int w = 0; w < NW; w++) {
-                    kw[w] = side.nk[w];
-                    vw[w] = side.nv[w];
-                    asm volatile("" : "+v"(kw[w]), "+v"(vw[w]));
-                }
-                if (lane * NPL < D) {
-#pragma unroll
-                    for (int e = 0; e < NPL; e++) {
-                        s_new[lane * NPL + e] = new_val(kw, e);
-                        s_new[D + lane * NPL + e] = new_val(vw, e);
-                    }
-                }
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the stores have landed in LDS
-                __builtin_amdgcn_wave_barrier();
-                const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * TILE;
-                const int r = (T - 1) & 15;
-                append_bf16_regs<D>(a, tile, s_new, r, q4, n, kr, vr);
-            }
         }
         // S^T[token 4q4+i][head n]
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -539,6 +526,37 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         }
     };
 
+    // Fused append: the owning piece's new-token block (the last streamed one, or when the token
+    // starts a block the one after it, whose id the piece loaded in lane nb when it has one) and
+    // the prefetch of its V tile into this wave's LDS area s_vt (LDS-direct loads: no registers
+    // held across the loop; a zero-sized descriptor for an invalid id writes zeros, never stored).
+    int abid = -1;
+    auto prefetch_vtile = [&]() {
+        if constexpr (APPEND) {
+            if (piece_owns_new<APPEND>(g)) {
+                if ((T & 15) != 0) {
+                    abid = __builtin_amdgcn_readlane(my_bid, nb - 1);
+                } else if (nb < kPieceBlocks) {
+                    abid = __builtin_amdgcn_readlane(my_bid, nb);
+                } else {  // a piece of 64 blocks has no lane for it: a table load here (rare)
+                    int zero = 0;
+                    asm volatile("" : "+v"(zero));  // a vector load (vmcnt), not a scalar one
+                    abid = __builtin_amdgcn_readfirstlane(
+                        a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + T / 16 + zero]);
+                }
+                abid = valid_bid(a, abid);
+                constexpr uint32_t kTileBytes = TILE * 2;
+                const int64_t tile = abid >= 0 ? (static_cast<int64_t>(abid) * Hkv + kvh) * kTileBytes : 0;
+                const u32x4_t rv = buffer_rsrc_words(static_cast<const char*>(a.v_cache) + tile,
+                                                     abid >= 0 ? kTileBytes : 0u);
+                const uint32_t base = lds_address(s_vt);
+#pragma unroll
+                for (uint32_t i = 0; i < (kTileBytes + 1023) / 1024; i++)
+                    lds_load16(rv, 16 * lane + 1024 * i, base + 1024 * i);
+            }
+        }
+    };
+
     if constexpr (decode_buffers(KV) != 3) {
         // NB rotating register buffers: NB - 1 blocks in flight while one is consumed (int8 blocks
         // carry half the bytes of bf16 ones, so more of them are kept in flight). No carry.
@@ -555,7 +573,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 load(kbuf[(b + NB - 1) % NB], vbuf[(b + NB - 1) % NB], j + NB - 1);
-                compute(kbuf[b], vbuf[b], j, false);
+                compute(kbuf[b], vbuf[b], j);
                 if (++j >= nb) break;
             }
         }
@@ -574,6 +592,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             // Items 0, 1 are in A, B and the side loads in `side` (issued by the previous piece,
             // or for a worker's first piece before it); the loop's last two iterations issue the
             // next piece's first two blocks.
+            prefetch_vtile();
             prefetch_next();
             side_next();
             prep_q();
@@ -582,13 +601,13 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             asm volatile("" ::"v"(my_bid), "v"(nxt_ids));
             do {
                 load(kx, vx, j + 2);
-                if (j < nb) compute(ka, va, j, false);
+                if (j < nb) compute(ka, va, j);
                 ++j;
                 load(ka, va, j + 2);
-                if (j < nb) compute(kb, vb, j, false);
+                if (j < nb) compute(kb, vb, j);
                 ++j;
                 load(kb, vb, j + 2);
-                if (j < nb) compute(kx, vx, j, false);
+                if (j < nb) compute(kx, vx, j);
                 ++j;
             } while (j < nbp);
             // Every vector memory access but the next piece's two blocks (the last 2 * LPI) has
@@ -597,46 +616,99 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             // next piece does not drain its carried loads to use them.
             __builtin_amdgcn_s_waitcnt(vmcnt_keep<2 * decode_block_loads<D, KV>()>());
         } else {
-            bool peeled = false;
-            if constexpr (APPEND) {
-                if (j_app >= 0) {
-                    // Iteration 0 (the appended block) is computed here, outside the loop: with the
-                    // patch inlined in the loop body the loop no longer fits the instruction cache
-                    // and every wave slows down. The loop then starts at iteration 1 with the same
-                    // buffer roles as usual.
-                    load(kx, vx, 0);
-                    load(ka, va, 1);
-                    load(kb, vb, 2);
-                    load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
-                    prefetch_next();
-                    prep_q();
-                    compute(kx, vx, 0, true);
-                    j = 1;
-                    peeled = true;
-                }
-            }
-            if (!peeled) {
-                load(ka, va, 0);
-                load(kb, vb, 1);
-                load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
-                prefetch_next();
-                prep_q();
-            }
+            load(ka, va, 0);
+            load(kb, vb, 1);
+            load_side<D, KV, QF32, APPEND, SHARED>(a, g, my_bid, true, side);
+            prefetch_vtile();
+            prefetch_next();
+            prep_q();
             while (j < nb) {
                 load(kx, vx, j + 2);
-                compute(ka, va, j, false);
+                compute(ka, va, j);
                 if (++j >= nb) break;
                 load(ka, va, j + 2);
-                compute(kb, vb, j, false);
+                compute(kb, vb, j);
                 if (++j >= nb) break;
                 load(kb, vb, j + 2);
-                compute(kx, vx, j, false);
+                compute(kx, vx, j);
                 ++j;
             }
+            // the V tile prefetch (older than the blocks just computed) has landed in LDS
+            if constexpr (APPEND) __builtin_amdgcn_s_waitcnt(vmcnt_keep<0>());
         }
     }
 
     if (!g.last) return;
+    if constexpr (APPEND) {
+        if (piece_owns_new<APPEND>(g)) {
+            // The new token joins the softmax with the values the cache holds after the append
+            // (bf16 by truncation), staged in LDS so every lane can read the dims it needs.
+            float kx[NPL], vx[NPL];
+#pragma unroll
+            for (int e = 0; e < NPL; e++) {
+                kx[e] = __uint_as_float(__float_as_uint(new_val(side.nk, e)) & 0xffff0000u);
+                vx[e] = __uint_as_float(__float_as_uint(new_val(side.nv, e)) & 0xffff0000u);
+            }
+            uint16_t* vt16 = reinterpret_cast<uint16_t*>(s_vt);
+            const int r = T & 15;
+            if (lane * NPL < D) {
+#pragma unroll
+                for (int e = 0; e < NPL; e++) {
+                    s_new[lane * NPL + e] = kx[e];
+                    s_new[D + lane * NPL + e] = vx[e];
+                    vt16[(lane * NPL + e) * 16 + r] = static_cast<uint16_t>(__float_as_uint(vx[e]) >> 16);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the stores have landed in LDS
+            __builtin_amdgcn_wave_barrier();
+            // Score of head n: q . k over this lane's dims of every slab, summed over the four
+            // lane groups of column n, then the scale (Q as the MFMA operands hold it).
+            float dot = 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < NSLAB; sl++) {
+                const int d0 = k_dim0<D, KV>(sl, q4);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float x = static_cast<float>(qhi[sl][e]);
+                    if constexpr (QF32) x += static_cast<float>(qlo[sl][e]);
+                    dot = __builtin_fmaf(x, s_new[d0 + e], dot);
+                }
+            }
+            const float sc = rows_sum(dot) * a.scale;
+            const float m_new = fmaxf(m_run, sc);
+            const float alpha = __expf(m_run - m_new);
+            const float pn = __expf(sc - m_new);
+            l_run = l_run * alpha + (q4 == 0 ? pn : 0.0f);
+            m_run = m_new;
+            float ar[4], pr[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ar[i] = __shfl(alpha, 4 * q4 + i, 64);
+                pr[i] = __shfl(pn, 4 * q4 + i, 64);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float vv = s_new[D + 16 * t + n];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(pr[i], vv, acc[t][i] * ar[i]);
+            }
+            // The cache: K row r as is, the V tile (patched in LDS above) in full lines.
+            if (abid >= 0) {
+                const int64_t tile = (static_cast<int64_t>(abid) * Hkv + kvh) * TILE;
+                uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache)) + tile + r * D;
+                if (lane * NPL < D) {
+#pragma unroll
+                    for (int e = 0; e < NPL; e++)
+                        kc[lane * NPL + e] = static_cast<uint16_t>(__float_as_uint(kx[e]) >> 16);
+                }
+                uint4* vg = reinterpret_cast<uint4*>(static_cast<uint16_t*>(const_cast<void*>(a.v_cache)) + tile);
+                const uint4* vl = reinterpret_cast<const uint4*>(s_vt);
+#pragma unroll
+                for (int i = 0; i < (TILE * 2 + 1023) / 1024; i++)
+                    if (lane + 64 * i < TILE * 2 / 16) vg[lane + 64 * i] = vl[lane + 64 * i];
+            }
+        }
+    }
     // ---- the portion ends: write it (lane (q4, n) holds O rows 4q4 .. 4q4 + 3, dims 16t + n) ----
     const float l_tot = rows_sum(l_run);  // head n's sum, in every lane of column n
     float M[4], L[4];                     // of head 4q4 + i, read from lane 4q4 + i (column 4q4 + i)
@@ -678,7 +750,8 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     constexpr int WAVES = decode_waves(D);
     constexpr int THREADS = 64 * WAVES;
     __shared__ MfmaShared<SHARED> sh;
-    __shared__ float s_app[WAVES][2 * D];  // per wave: the appended token's K and V values
+    __shared__ float s_app[APPEND ? WAVES : 1][2 * D];  // per wave: the appended token's K and V values
+    __shared__ uint4 s_vtile[APPEND ? WAVES : 1][APPEND ? D * 16 * 2 / 16 : 1];  // per wave: a V tile
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -732,7 +805,9 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
                     sh.qinfo[r] = (ok ? first : 0) | (ok ? nm : 1) << 16 | 1 << 24;
                 }
             } else {
-                const int T = clamp_len(a, raw[k]);
+                // Fused append: the row streams its first T - 1 tokens; the new token at T - 1
+                // joins at the end (T == 1: nothing streamed, see below).
+                const int T = clamp_len(a, raw[k]) - (APPEND ? 1 : 0);
                 sh.lens[r] = T;
                 c = T <= 0 ? 0 : (T + 15) / 16;
                 if constexpr (SHARED) {
@@ -771,10 +846,33 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     __syncthreads();
 
     const int Hkv = a.num_kv_heads;
-    // Sequences with no context produce zeros.
+    // Sequences with no context produce zeros. Fused append: a sequence whose only token is the new
+    // one (context length 1) produces that token's V (bf16 by truncation) in every head of its KV
+    // head, and the token is written into row 0 of its first block.
     for (int s = blockIdx.x; s < num_seqs; s += gridDim.x) {
         if (sh.lens[NG + s] > 0) continue;
         const int n = Hkv * a.group * D;
+        if (APPEND && sh.lens[NG + s] == 0) {
+            const bool f32 = !a.q_bf16;
+            for (int idx = tid; idx < n; idx += THREADS) {
+                const int kvh = idx / (a.group * D), d = idx % D;
+                const float v = act_at(a.v_new, f32, (static_cast<int64_t>(s) * Hkv + kvh) * D + d);
+                a.out[static_cast<int64_t>(s) * n + idx] = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+            }
+            const int bid = a.block_tables[static_cast<int64_t>(s) * a.max_blocks_per_seq];
+            if (bid >= 0 && bid < a.num_blocks) {
+                uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache));
+                uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache));
+                for (int idx = tid; idx < Hkv * D; idx += THREADS) {
+                    const int kvh = idx / D, d = idx % D;
+                    const int64_t src = (static_cast<int64_t>(s) * Hkv + kvh) * D + d;
+                    const int64_t tile = (static_cast<int64_t>(bid) * Hkv + kvh) * 16 * D;
+                    kc[tile + d] = pa::bf16_trunc(act_at(a.k_new, f32, src));
+                    vc[tile + d * 16] = pa::bf16_trunc(act_at(a.v_new, f32, src));
+                }
+            }
+            continue;
+        }
         for (int idx = tid; idx < n; idx += THREADS) a.out[static_cast<int64_t>(s) * n + idx] = 0.0f;
     }
 
@@ -881,16 +979,17 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     };
     RowState<D / 16> st;
     st.reset();
-    float* s_new = &s_app[wave][0];
+    float* s_new = &s_app[APPEND ? wave : 0][0];
+    uint4* s_vt = &s_vtile[APPEND ? wave : 0][0];
     PipeBufs<D, KV> bufs;
     PieceSide<D, QF32> side, nside;
     // Pieces in flight: cur (streaming), nxt (ids loaded during the previous piece) and nxt2 (ids
     // loaded during this one).
     Piece cur, nxt;
     next_piece(cur);
-    int cur_ids = piece_ids(a, cur, lane);
+    int cur_ids = piece_ids_of<APPEND>(a, cur, lane);
     bool has_next = next_piece(nxt);
-    int nxt_ids = has_next ? piece_ids(a, nxt, lane) : -1;
+    int nxt_ids = has_next ? piece_ids_of<APPEND>(a, nxt, lane) : -1;
     // The first piece waits for its ids anyway; waiting for both here lets the compiler treat the
     // ids a piece receives as loaded on every path into the loop.
     asm volatile("" ::"v"(cur_ids), "v"(nxt_ids));
@@ -909,10 +1008,10 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
         Piece nxt2;
         bool has_next2 = false;
         int nxt2_ids = -1;
-        mfma_piece<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, side, bufs, st, s_new, has_next, nxt,
+        mfma_piece<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, side, bufs, st, s_new, s_vt, has_next, nxt,
                                                 nxt_ids, nside, [&]() {
                                                     if (has_next) has_next2 = next_piece(nxt2);
-                                                    if (has_next2) nxt2_ids = piece_ids(a, nxt2, lane);
+                                                    if (has_next2) nxt2_ids = piece_ids_of<APPEND>(a, nxt2, lane);
                                                 });
         if (!has_next) break;
         cur = nxt;

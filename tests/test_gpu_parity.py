@@ -422,8 +422,9 @@ def test_decode_invalid_block_ids_read_as_zero(stream):
 APPEND_LENS = [1, 2, 16, 17, 33, 100, 256, 257, 300, 513, 1000, 1024, 1025, 2000]
 
 
-# Long rows: segments of up to 256 blocks (64 per wave), the appended block at a late lane.
-LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000]
+# Long rows: segments of up to 256 blocks (64 per wave), the appended block at a late lane;
+# 1025 and 2049 put the fused append's new token in the block after a piece of exactly 64 blocks.
+LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000, 1025, 2049]
 
 
 @pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D,part,lens", [
