@@ -62,7 +62,11 @@ struct DecodeArgs {
     // MFMA kernel: > 0 cuts every row (sequence, KV head) into this many partitions of whole
     // blocks instead of the batch-wide equal ranges (pa_config.num_splits)
     int32_t num_splits;
+    // Fused append (bf16 caches) when the merge kernel runs: the decode folds the new token into
+    // attention from k_new / v_new and the merge kernel writes it into the cache.
+    int32_t append_in_merge;
 };
+
 
 // Shared-prefix plan, in device memory: num_groups records {first sequence, members, shared
 // blocks}, then per sequence {group or -1, shared blocks or 0}. The members of a group are
@@ -77,6 +81,38 @@ constexpr int kPrefixSlotRows = 16;
 // Context length clamped to what the table holds and to max_context_len (raw: context_lens[seq]).
 __device__ __forceinline__ int clamp_len(const DecodeArgs& a, int raw) {
     return min(min(raw, a.max_blocks_per_seq * pa::kBlockSize), a.max_context_len);
+}
+
+// Element i of an activation array (the fused append's new K/V): fp32, or bf16 widened exactly.
+__device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
+    return f32 ? static_cast<const float*>(p)[i] : pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// The new token (position T - 1 of sequence seq, KV head kvh; T = its clamped context length >= 2)
+// written into a bf16 cache as pa_kv_append stores it: K row (T - 1) % 16 and V column (T - 1) % 16
+// of the block the table gives for it, bf16 by truncation. One wave, lane l takes dims l, l + 64, ..
+// Written by the merge kernel, after the decode's streaming, with non-temporal stores: the V column
+// touches one line per two dims of the transposed tile, and written among the decode's reads, or
+// left dirty in the caches for the next step's reads to evict, those lines cost the C2 step 3-4 us
+// (measured: in the decode, in the merge kernel with plain stores, as whole tiles read and
+// rewritten; non-temporal 2-byte stores here cost the least).
+template <int D>
+__device__ __forceinline__ void append_token_bf16(const DecodeArgs& a, int seq, int kvh) {
+    const int T = clamp_len(a, a.context_lens[seq]);
+    if (T < 2) return;  // T == 1: the decode writes it (no streamed block); T <= 0: nothing
+    const int bid = a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + (T - 1) / 16];
+    if (bid < 0 || bid >= a.num_blocks) return;
+    const int lane = threadIdx.x & 63, r = (T - 1) & 15;
+    const bool f32 = !a.q_bf16;
+    const int64_t src = (static_cast<int64_t>(seq) * a.num_kv_heads + kvh) * D;
+    const int64_t tile = (static_cast<int64_t>(bid) * a.num_kv_heads + kvh) * 16 * D;
+    uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache)) + tile;
+    uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache)) + tile;
+#pragma unroll
+    for (int d = lane; d < D; d += 64) {
+        __builtin_nontemporal_store(pa::bf16_trunc(act_at(a.k_new, f32, src + d)), kc + r * D + d);
+        __builtin_nontemporal_store(pa::bf16_trunc(act_at(a.v_new, f32, src + d)), vc + d * 16 + r);
+    }
 }
 
 // Final write of one (sequence, query head, dim): normalised output, or the partition's partial.
@@ -285,6 +321,7 @@ __device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const DecodeArgs a, int32_t num_seqs) {
     const int kvh = blockIdx.x, seq = blockIdx.y;
+    if (a.append_in_merge && threadIdx.x >= 192) append_token_bf16<D>(a, seq, kvh);  // the last wave
     const int64_t R0 = a.ws_pref[seq];
     const int nbr = a.ws_pref[seq + 1] - a.ws_pref[seq];
     const int64_t total = a.ws_pref[num_seqs];
@@ -413,10 +450,6 @@ __device__ __forceinline__ int k_dim0(int sl, int q4) {
     return KV == PA_DTYPE_INT8 ? (D / 4) * q4 + 8 * sl : 32 * sl + 8 * q4;
 }
 
-// Element i of an activation array (the fused append's new K/V): fp32, or bf16 widened exactly.
-__device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
-    return f32 ? static_cast<const float*>(p)[i] : pa::bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
 
 // Word 3 of a raw buffer descriptor on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferFlags = 0x00020000;

@@ -22,12 +22,13 @@
 //
 // Fused append (pa_paged_decode_append, bf16 caches): a row streams its first T - 1 cached tokens
 // only; the new token (position T - 1, from k_new / v_new) joins the softmax as one more element at
-// the end of the row portion that holds the row's last streamed block, and that portion's wave
-// writes it into the cache: its K row as is, its V column by rewriting the whole V tile (fetched
-// into LDS when the piece starts, patched there, stored back as full lines -- 2-byte stores at a
-// 32-byte stride, one per dim, cost the step about 3 us of partial-line writes). No block is
-// patched in registers, so the fused kernel streams with the same loop (and carry) as the plain
-// decode.
+// the end of the row portion that holds the row's last streamed block. No block is patched in
+// registers, so the fused kernel streams with the same loop (and carry) as the plain decode. The
+// token is written into the cache by the split-merge kernel that follows the decode
+// (append_in_merge): written here, among the decode's reads, the V column (one line per dim of
+// the tile) cost the step about 3 us whatever the form of the stores. Without a merge launch
+// (a single range) the owning wave writes it: its K row as is, its V column by rewriting the
+// whole V tile, fetched into LDS when the piece starts, patched there and stored back.
 //
 // Per block: S^T[16 tokens][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16 (query heads padded
 // to 16 rows), online softmax in fp32, O[16 heads][D] += P . V on v_mfma_f32_16x16x16_bf16 with P
@@ -147,6 +148,10 @@ template <int D, int KV, bool QF32, bool APPEND>
 __host__ __device__ constexpr bool decode_carry() {
     return decode_buffers(KV) == 3 && !QF32 && D <= 128;
 }
+
+// Leading empty iterations of a carried piece of nb blocks: its iteration count nb + lead is a
+// multiple of 3, the unroll of the three-buffer loop.
+__device__ __forceinline__ int piece_lead(int nb) { return (3 - nb % 3) % 3; }
 
 // Fused append (pa_paged_decode_append, bf16 caches): Piece::T counts the streamed tokens, the
 // new token sits at position T; the piece that ends the portion holding the row's last streamed
@@ -398,13 +403,18 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         }
     };
 
-    // The next piece (carry): its block count and this piece's padded iteration count nbp, the
-    // smallest multiple of 3 >= max(nb, 3). Iterations nb .. nbp - 1 compute nothing; item nbp + k
-    // is the next piece's block k, loaded into buffer (nbp + k) % 3 = k, where the next piece reads
-    // it. The next piece's side loads go out at this piece's start (its ids were loaded during the
-    // previous piece).
-    const int nbp = CARRY ? (max(nb, 3) + 2) / 3 * 3 : nb;
+    // The next piece (carry): its block count and this piece's iteration count nbp, a multiple of 3
+    // (the loop is unrolled over the three buffers). A piece is padded at its front: its first
+    // `lead` = piece_lead(nb) iterations compute nothing and iteration j computes block j - lead,
+    // so the last two iterations compute the piece's last blocks while loading the next piece's
+    // iterations 0 and 1 (item nbp + k, buffer k): the pipeline stays full across the boundary.
+    // (Padded at the end instead, a piece of 3k + 1 or 3k + 2 blocks issued the next piece's first
+    // loads only after its last compute: a memory latency per boundary.) The next piece's side
+    // loads go out at this piece's start (its ids were loaded during the previous piece).
+    const int lead = CARRY ? piece_lead(nb) : 0;
+    const int nbp = nb + lead;
     const int nnb = CARRY && has_next ? nxt.b1 - nxt.b0 : 0;
+    const int nlead = piece_lead(nnb);
     auto side_next = [&]() {
         if constexpr (CARRY) {
             if (has_next) load_side<D, KV, QF32, APPEND, SHARED>(a, nxt, nxt_ids, true, nside);
@@ -413,14 +423,15 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
 
     using KR = typename Raw::K;
     using VR = typename Raw::V;
-    // Item i: block entry(i) of this piece (i < nb), nothing (nb <= i < nbp) or block i - nbp of
-    // the next piece (zero-sized past its list).
+    // Item i (iteration i's block): block i - lead of this piece (lead <= i < nbp), nothing (the
+    // lead), or the next piece's iteration i - nbp (its block i - nbp - nlead; zero-sized past
+    // its list).
     auto load = [&](KR (&kr)[NSLAB], VR (&vr)[NT], int i) {
         int bid = -1, kv = kvh;
-        if (i < nb) {
-            bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, entry(i) & 63));
-        } else if (CARRY && i >= nbp && i - nbp < nnb) {
-            bid = valid_bid(a, __builtin_amdgcn_readlane(nxt_ids, i - nbp));
+        if (i >= lead && i < nbp) {
+            bid = valid_bid(a, __builtin_amdgcn_readlane(my_bid, entry(i - lead) & 63));
+        } else if (CARRY && i >= nbp + nlead && i - nbp - nlead < nnb) {
+            bid = valid_bid(a, __builtin_amdgcn_readlane(nxt_ids, i - nbp - nlead));
             kv = nxt.kvh;
         }
         load_block<D, KV>(a, kr, vr, bid, kv);
@@ -533,7 +544,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     int abid = -1;
     auto prefetch_vtile = [&]() {
         if constexpr (APPEND) {
-            if (piece_owns_new<APPEND>(g)) {
+            if (piece_owns_new<APPEND>(g) && !a.append_in_merge) {
                 if ((T & 15) != 0) {
                     abid = __builtin_amdgcn_readlane(my_bid, nb - 1);
                 } else if (nb < kPieceBlocks) {
@@ -601,13 +612,13 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             asm volatile("" ::"v"(my_bid), "v"(nxt_ids));
             do {
                 load(kx, vx, j + 2);
-                if (j < nb) compute(ka, va, j);
+                if (j >= lead) compute(ka, va, j - lead);
                 ++j;
                 load(ka, va, j + 2);
-                if (j < nb) compute(kb, vb, j);
+                if (j >= lead) compute(kb, vb, j - lead);
                 ++j;
                 load(kb, vb, j + 2);
-                if (j < nb) compute(kx, vx, j);
+                if (j >= lead) compute(kx, vx, j - lead);
                 ++j;
             } while (j < nbp);
             // Every vector memory access but the next piece's two blocks (the last 2 * LPI) has
@@ -692,8 +703,9 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(pr[i], vv, acc[t][i] * ar[i]);
             }
-            // The cache: K row r as is, the V tile (patched in LDS above) in full lines.
-            if (abid >= 0) {
+            // The cache (unless the merge kernel writes the token): K row r as is, the V tile
+            // (patched in LDS above) in full lines.
+            if (abid >= 0 && !a.append_in_merge) {
                 const int64_t tile = (static_cast<int64_t>(abid) * Hkv + kvh) * TILE;
                 uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache)) + tile + r * D;
                 if (lane * NPL < D) {
@@ -997,10 +1009,13 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
         // The first piece's carried loads: its side loads, then its first two blocks. Waiting for
         // all but the blocks here puts the side values in registers on every path into the loop,
         // so no later piece waits on them (with its carried blocks in flight).
-        const int nb0 = cur.b1 - cur.b0;
+        // Iterations 0 and 1 of the piece: blocks 0 - lead and 1 - lead (nothing for the lead).
+        const int nb0 = cur.b1 - cur.b0, lead0 = piece_lead(nb0);
         load_side<D, KV, QF32, APPEND, SHARED>(a, cur, cur_ids, true, side);
-        load_block<D, KV>(a, bufs.k[0], bufs.v[0], valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 0)), cur.kvh);
-        load_block<D, KV>(a, bufs.k[1], bufs.v[1], nb0 > 1 ? valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 1)) : -1,
+        load_block<D, KV>(a, bufs.k[0], bufs.v[0], lead0 == 0 ? valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 0)) : -1,
+                          cur.kvh);
+        load_block<D, KV>(a, bufs.k[1], bufs.v[1],
+                          lead0 <= 1 && 1 - lead0 < nb0 ? valid_bid(a, __builtin_amdgcn_readlane(cur_ids, 1 - lead0)) : -1,
                           cur.kvh);
         __builtin_amdgcn_s_waitcnt(vmcnt_keep<2 * decode_block_loads<D, KV>()>());
     }

@@ -278,6 +278,10 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     }
     const bool qf32 = cfg->q_dtype == PA_DTYPE_FP32;
     const int64_t max_grid = max_units > 0 ? max_units : 1;
+    // The merge kernel runs when there is more than one range (a row may span two); a fused bf16
+    // append then has it write the new tokens into the cache.
+    const bool merge = max_units > cfg->num_kv_heads;
+    a.append_in_merge = append && cfg->kv_dtype == PA_DTYPE_BF16 && merge ? 1 : 0;
     if (append && cfg->kv_dtype == PA_DTYPE_INT8 && num_seqs > 0) {
         const int threads = pa::append_int8_threads(cfg->num_kv_heads);
         switch (cfg->head_dim) {
@@ -295,7 +299,7 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
         default: pa::launch_decode_mfma<256>(a, cfg->kv_dtype, qf32, append, false, num_seqs, max_grid, s); break;
     }
     PA_HIP_CHECK(hipGetLastError());
-    if (max_units > cfg->num_kv_heads) {  // more than one range: a row may span two
+    if (merge) {
         dim3 mgrid(cfg->num_kv_heads, num_seqs);
         switch (cfg->head_dim) {
             case 32: pa::paged_decode_merge_split_kernel<32><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
