@@ -132,6 +132,103 @@ __device__ __forceinline__ void append_int8_apply(const void* src, bool in_bf16,
     }
 }
 
+// One token appended alone into its block (the block receives no other token of the call), by one
+// wave for (KV head h, K or V): the same bytes and statistics as append_int8_apply with a one-token
+// segment, in fewer memory round trips. x holds the token's values (lane l: dims l, l + 64, ..),
+// loaded by the caller before the slot was known. The block's statistics and its codes come in one
+// round trip; the token's codes are merged into the tile's 16-byte chunks (V: byte off of the chunk
+// of each dim, the lane's own dims; K: row off's chunks, staged through `stage`, D bytes of LDS), so
+// the tile goes back in one set of whole-chunk stores with no store-then-wait ordering between the
+// requantised rows and the token's row.
+template <int D>
+__device__ __forceinline__ void append_int8_one_token(const float (&x)[D / 64], int64_t slot, int8_t* cache,
+                                                      float* scale, float* absmax, int h, int32_t num_kv_heads,
+                                                      bool is_v, int8_t* stage) {
+#pragma clang fp contract(off)
+    constexpr int kPer = D / 64;
+    constexpr int kChunks = kBlockSize * D / 16 / 64;  // 16-byte chunks of the tile per lane (= kPer)
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = slot / kBlockSize;
+    const int off = static_cast<int>(slot % kBlockSize);
+    const int64_t sidx = blk * num_kv_heads + h;
+    int8_t* block_codes = cache + ((blk * num_kv_heads + h) * kBlockSize) * D;
+    uint4* chunks = reinterpret_cast<uint4*>(block_codes);
+    const float amax_mem = absmax[sidx];
+    const float scale_mem = scale[sidx];
+    uint4 ch[kChunks];
+#pragma unroll
+    for (int i = 0; i < kChunks; i++) ch[i] = chunks[lane + 64 * i];
+    float seg_amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+        const float a = fabsf(x[k]);
+        seg_amax = a > seg_amax ? a : seg_amax;  // NaN never wins, as `if (a > m) m = a`
+    }
+    seg_amax = wave_max(seg_amax);
+    const bool fresh = off == 0;  // writing row 0 starts the block afresh
+    float cur_scale;
+    bool grow = false, new_stats = false;
+    float old_scale = 0.0f, amax = 0.0f;
+    if (fresh) {
+        amax = seg_amax;
+        cur_scale = seg_amax / 127.0f;
+        new_stats = true;
+    } else {
+        amax = amax_mem;
+        cur_scale = scale_mem;
+        if (seg_amax > amax) {
+            old_scale = cur_scale;
+            cur_scale = seg_amax / 127.0f;
+            amax = seg_amax;
+            grow = true;
+            new_stats = true;
+        }
+    }
+    // the token's codes: lane l, dims l + 64 k
+    uint32_t code[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; k++) code[k] = static_cast<uint32_t>(static_cast<uint8_t>(quantize_symmetric(x[k], cur_scale)));
+    if (!is_v) {  // K row off: D consecutive bytes, chunks off * D / 16 .. (+ D / 16), via LDS
+#pragma unroll
+        for (int k = 0; k < kPer; k++) stage[lane + 64 * k] = static_cast<int8_t>(code[k]);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int i = 0; i < kChunks; i++) {
+        const int c = lane + 64 * i;  // K: row c / (D / 16), dims 16 (c % (D / 16)) ..; V: dim c, tokens 0 .. 15
+        uint32_t w[4] = {ch[i].x, ch[i].y, ch[i].z, ch[i].w};
+        if (grow) {
+            // QuantizeSymmetric(Dequantize(q, old_scale), new_scale) on every row but `off`
+#pragma unroll
+            for (int b = 0; b < 16; b++) {
+                const int row = is_v ? b : c / (D / 16);
+                if (row == off) continue;
+                const uint32_t sh = 8 * (b & 3);
+                const int32_t q = static_cast<int32_t>(w[b >> 2] << (24 - sh)) >> 24;
+                const float deq = static_cast<float>(q) * old_scale;
+                const uint32_t nq = static_cast<uint32_t>(static_cast<uint8_t>(quantize_symmetric(deq, cur_scale)));
+                w[b >> 2] = (w[b >> 2] & ~(0xffu << sh)) | (nq << sh);
+            }
+        }
+        if (is_v) {  // byte off of dim c's chunk: this lane's own code of dim c = lane + 64 i
+            const uint32_t sh = 8 * (off & 3);
+            w[off >> 2] = (w[off >> 2] & ~(0xffu << sh)) | (code[i] << sh);
+        } else if (c / (D / 16) == off) {  // a chunk of row off: 16 codes from the stage
+            const uint4 n = *reinterpret_cast<const uint4*>(stage + 16 * (c % (D / 16)));
+            w[0] = n.x;
+            w[1] = n.y;
+            w[2] = n.z;
+            w[3] = n.w;
+        }
+        chunks[c] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    if (new_stats && lane == 0) {
+        absmax[sidx] = amax;
+        scale[sidx] = cur_scale;
+    }
+}
+
 // Segments collected per pass of the owner's scan (a block has at most 16 rows, so more than one
 // pass only happens when slots repeat).
 constexpr int kAppendSegList = 64;

@@ -146,6 +146,20 @@ template <int D>
 __global__ __launch_bounds__(pa::kAppendMaxThreads) void append_last_token_int8_kernel(const DecodeArgs a,
                                                                                       int32_t num_seqs) {
     const int64_t capacity = static_cast<int64_t>(a.num_blocks) * pa::kBlockSize;
+    const int i = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int Hkv = a.num_kv_heads;
+    // Wave p < 2 Hkv: KV head p / 2, K (p even) or V. Its token values first: they do not depend on
+    // the slot, so they are in flight with the slot lookups below.
+    const int h = wave >> 1;
+    const bool is_v = (wave & 1) != 0;
+    float x[D / 64];
+    if (wave < 2 * Hkv) {
+        const int64_t src = (static_cast<int64_t>(i) * Hkv + h) * D;
+#pragma unroll
+        for (int k = 0; k < D / 64; k++) x[k] = pa::load_act(is_v ? a.v_new : a.k_new, a.q_bf16 != 0, src + lane + 64 * k);
+    }
     auto last_slot = [&](int t) -> int64_t {
         const int T = clamp_len(a, a.context_lens[t]);
         if (T <= 0) return -1;
@@ -153,16 +167,45 @@ __global__ __launch_bounds__(pa::kAppendMaxThreads) void append_last_token_int8_
         return bid >= 0 ? static_cast<int64_t>(bid) * pa::kBlockSize + (T - 1) % pa::kBlockSize : -1;
     };
     // Every sequence's slot, looked up once by the workgroup (two dependent loads each, all in
-    // flight together): the owner's scans then read LDS.
+    // flight together): the ownership checks read LDS.
     __shared__ int64_t s_slot[pa::kMaxPersistentSeqs];
-    for (int t = threadIdx.x; t < num_seqs; t += blockDim.x) s_slot[t] = last_slot(t);
+    __shared__ __align__(16) int8_t s_stage[pa::kAppendMaxThreads / 64][D];
+    for (int t = tid; t < num_seqs; t += blockDim.x) s_slot[t] = last_slot(t);
     __syncthreads();
     auto slot_at = [&](int t) -> int64_t { return s_slot[t]; };
-    pa::append_int8_block<D>(a.k_new, a.v_new, a.q_bf16 != 0, static_cast<int64_t>(a.num_kv_heads) * D, slot_at,
-                             static_cast<int32_t>(blockIdx.x), num_seqs,
-                             static_cast<int8_t*>(const_cast<void*>(a.k_cache)),
-                             static_cast<int8_t*>(const_cast<void*>(a.v_cache)), const_cast<float*>(a.k_scale),
-                             const_cast<float*>(a.v_scale), a.k_absmax, a.v_absmax, a.num_kv_heads, capacity);
+    // The usual case: no other token of the call lands in this token's block, which is then
+    // appended by append_int8_one_token; otherwise the general owner path (append_int8_block).
+    const int64_t my = s_slot[i];
+    const bool valid = my >= 0 && my < capacity;
+    bool shared = false;
+    if (valid) {
+        for (int t = tid; t < num_seqs; t += blockDim.x) {
+            const int64_t sl = s_slot[t];
+            shared |= t != i && sl >= 0 && sl < capacity && sl / pa::kBlockSize == my / pa::kBlockSize;
+        }
+    }
+    if (__syncthreads_or(shared)) {
+        pa::append_int8_block<D>(a.k_new, a.v_new, a.q_bf16 != 0, static_cast<int64_t>(Hkv) * D, slot_at,
+                                 static_cast<int32_t>(blockIdx.x), num_seqs,
+                                 static_cast<int8_t*>(const_cast<void*>(a.k_cache)),
+                                 static_cast<int8_t*>(const_cast<void*>(a.v_cache)), const_cast<float*>(a.k_scale),
+                                 const_cast<float*>(a.v_scale), a.k_absmax, a.v_absmax, Hkv, capacity);
+        return;
+    }
+    if (!valid) return;
+    const int nwaves = static_cast<int>(blockDim.x) >> 6;
+    for (int p = wave; p < 2 * Hkv; p += nwaves) {  // more than 8 KV heads: a wave takes several
+        const int hp = p >> 1;
+        const bool vp = (p & 1) != 0;
+        if (p != wave) {
+            const int64_t src = (static_cast<int64_t>(i) * Hkv + hp) * D;
+#pragma unroll
+            for (int k = 0; k < D / 64; k++) x[k] = pa::load_act(vp ? a.v_new : a.k_new, a.q_bf16 != 0, src + lane + 64 * k);
+        }
+        pa::append_int8_one_token<D>(x, my, static_cast<int8_t*>(const_cast<void*>(vp ? a.v_cache : a.k_cache)),
+                                     const_cast<float*>(vp ? a.v_scale : a.k_scale), vp ? a.v_absmax : a.k_absmax, hp,
+                                     Hkv, vp, &s_stage[wave][0]);
+    }
 }
 
 }  // namespace

@@ -332,6 +332,43 @@ def test_append_int8_requantisation_all_codes(stream, old_scale, new_amax):
         np.testing.assert_array_equal(to_np(dev[n]), a, err_msg=n)
 
 
+def test_decode_append_int8_shared_last_block(stream):
+    """Fused int8 append where several sequences' new tokens land in one block (their tables share
+    the block at different rows, and one row twice): the workgroup of the first such token owns
+    the block and applies the tokens in sequence order (the general path); the others take the
+    one-token path. Bytes, scales and absmax against the oracle's pa_kv_append in call order."""
+    lens = [20, 24, 40, 33, 1, 17, 300]
+    w = wl.make_small(91, num_seqs=len(lens), lens=lens, Hq=16, Hkv=4, D=128, kv_dtype=2, q_dtype=1)
+    w.block_tables[1, 1] = w.block_tables[0, 1]  # seq 1's last token (row 7) in seq 0's last block (row 3)
+    w.block_tables[3, 2] = w.block_tables[0, 1]  # seq 3's last token at row 0 of that block: afresh
+    inp = wl.numpy_inputs(w, 92)
+    cfg = config_for(w)
+    S, Hkv, D = w.num_seqs, w.num_kv_heads, w.head_dim
+    rng = np.random.default_rng(93)
+    k_new = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    v_new = rng.standard_normal((S, Hkv, D), dtype=np.float32)
+    k_new[1, :, 3] *= 8.0  # growth on the shared block
+    k_new, v_new = orc.bf16_from_f32(k_new), orc.bf16_from_f32(v_new)
+    pos = w.context_lens.astype(np.int64) - 1
+    slots = w.block_tables[np.arange(S), pos // 16].astype(np.int64) * 16 + pos % 16
+    host, g = build_int8_caches(w, inp, stream)
+    hk, hv = host["k_cache"].copy(), host["v_cache"].copy()
+    hks, hvs = host["k_scale"].copy(), host["v_scale"].copy()
+    hka, hva = to_np(g["ka"]).copy(), to_np(g["va"]).copy()
+    orc.kv_append(cfg, k_new, v_new, slots, hk, hv, hks, hvs, hka, hva)
+    out = empty_gpu((S, w.num_q_heads, D), np.float32)
+    wsb = pa.decode_workspace_size(cfg, S, w.max_context_len)
+    ws = empty_gpu((max(wsb, 1),), np.uint8)
+    pa.paged_decode_append(stream, cfg, out, to_gpu(inp["q"]), to_gpu(k_new), to_gpu(v_new), g["kc"], g["vc"], g["ks"],
+                           g["vs"], g["ka"], g["va"], to_gpu(w.block_tables), to_gpu(w.context_lens), S, w.max_blocks,
+                           w.max_context_len, ws, wsb)
+    _sync()
+    for n, want in dict(kc=hk, vc=hv, ks=hks, vs=hvs, ka=hka, va=hva).items():
+        np.testing.assert_array_equal(to_np(g[n]), want, err_msg=n)
+    ref = orc.paged_decode(cfg, inp["q"], hk, hv, hks, hvs, w.block_tables, w.context_lens, n_threads=NTHREADS)
+    check_close(to_np(out), ref, **tol_for(2), what="int8 fused append, shared last block")
+
+
 # ---- decode -----------------------------------------------------------------------------------------
 def test_decode_c1_fp32(stream):
     """C1, the CPU-parity configuration (fp32 cache and query, VALU kernel), at the fp32 bar."""
