@@ -335,7 +335,11 @@ pa_status pa_paged_decode_prefix(pa_stream* stream, const pa_config* cfg, float*
  * Query i attends to keys 0 .. prefix_lens[s] + i (bottom-right aligned causal mask,
  * StandardPagedAttentionKernel.cs:219-255); see PA_FLAG_REFERENCE_LITERAL_MASK.
  *   out: [total_q][num_q_heads][head_dim] fp32, q: [total_q][num_q_heads][head_dim] of
- *   cfg->q_dtype (BF16 or FP32); the cache must be BF16 or INT8.
+ *   cfg->q_dtype (BF16 or FP32); caches of any kv_dtype. BF16 and INT8 caches take head_dim 64,
+ *   128 or 256 and compute on bf16 / fp16 MFMA operands; FP32 caches (head_dim 32 .. 256) compute
+ *   in fp32 throughout (fp32 MFMA operands and accumulation), which is what the dense
+ *   ComputePagedAttention of IPagedAttentionKernel (Kernels/IPagedAttentionKernel.cs:13-28) needs
+ *   for more than one query: one launch over the prompt instead of one decode row per query.
  *   max_chunk_len: host-side upper bound of the chunk lengths.
  * Range: every finite cache value is accepted. The P.V product runs on fp16 operands; int8
  * caches fold log2 of each block's V scale into the softmax exponent, so P times the scale stays

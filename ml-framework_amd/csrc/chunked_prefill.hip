@@ -751,15 +751,18 @@ extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg,
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: chunks need at least one block per sequence");
     if (!out || !q || !q_start_loc || !prefix_lens || !k_cache || !v_cache || !block_tables)
         return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: null pointer");
-    if (cfg->kv_dtype == PA_DTYPE_FP32)
-        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: the cache must be BF16 or INT8");
-    if (cfg->head_dim < 64)
-        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: head_dim must be 64, 128 or 256");
-    if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
-        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: int8 cache needs k_scale and v_scale");
     const uint32_t masks = cfg->flags & (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK);
     if (masks == (PA_FLAG_REFERENCE_LITERAL_MASK | PA_FLAG_NO_MASK))
         return pa::set_error(PA_ERROR_INVALID_CONFIG, "pa_chunked_prefill: conflicting mask flags");
+    const int32_t mask_mode = (cfg->flags & PA_FLAG_NO_MASK) ? 2 : ((cfg->flags & PA_FLAG_REFERENCE_LITERAL_MASK) ? 1 : 0);
+    if (cfg->kv_dtype == PA_DTYPE_FP32)
+        return pa::launch_chunked_prefill_fp32(pa::native(stream), cfg, out, q, q_start_loc, prefix_lens,
+                                               static_cast<const float*>(k_cache), static_cast<const float*>(v_cache),
+                                               block_tables, num_seqs, max_blocks_per_seq, max_chunk_len, mask_mode);
+    if (cfg->head_dim < 64)
+        return pa::set_error(PA_ERROR_UNSUPPORTED, "pa_chunked_prefill: bf16 and int8 caches take head_dim 64, 128 or 256");
+    if (cfg->kv_dtype == PA_DTYPE_INT8 && (!k_scale || !v_scale))
+        return pa::set_error(PA_ERROR_INVALID_ARGUMENT, "pa_chunked_prefill: int8 cache needs k_scale and v_scale");
 
     pa::PrefillArgs a{};
     a.out = out;
@@ -775,7 +778,7 @@ extern "C" pa_status pa_chunked_prefill(pa_stream* stream, const pa_config* cfg,
     a.group = cfg->num_q_heads / cfg->num_kv_heads;
     a.max_blocks_per_seq = max_blocks_per_seq;
     a.num_blocks = cfg->num_blocks;
-    a.mask_mode = (cfg->flags & PA_FLAG_NO_MASK) ? 2 : ((cfg->flags & PA_FLAG_REFERENCE_LITERAL_MASK) ? 1 : 0);
+    a.mask_mode = mask_mode;
     a.scale = pa::resolve_scale(cfg);
 
     a.qtiles_per_wg = a.group >= pa::kPrefillUnits ? 1 : pa::kPrefillUnits / a.group;

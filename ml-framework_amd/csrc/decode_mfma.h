@@ -922,9 +922,10 @@ __global__ __launch_bounds__(64 * decode_waves(D), D > 128 ? 1 : 2) void paged_d
     // fewer than k + 1 partitions' worth of blocks).
     auto split_range = [&](int64_t su, int64_t& pp, int64_t& ee) {
         const int64_t sr = su / Hkv;
-        const int sq = static_cast<int>(sr / NSP), k = static_cast<int>(sr - static_cast<int64_t>(sq) * NSP);
+        const int ns = NSP > 0 ? NSP : 1;  // only called with NSP > 0
+        const int sq = static_cast<int>(sr / ns), k = static_cast<int>(sr - static_cast<int64_t>(sq) * ns);
         const int nbr = sh.pref[sq + 1] - sh.pref[sq];
-        const int c = (nbr + NSP - 1) / NSP;
+        const int c = (nbr + ns - 1) / ns;
         pp = sh.pref[sq] + min(nbr, k * c);
         ee = sh.pref[sq] + min(nbr, (k + 1) * c);
     };

@@ -54,6 +54,12 @@ pa_status launch_kv_append(const char* f, hipStream_t s, const pa_config* cfg, c
                            void* k_cache, void* v_cache, float* k_scale, float* v_scale, float* k_absmax,
                            float* v_absmax);
 
+// pa_chunked_prefill over an fp32 cache (chunked_prefill_fp32.hip); the caller has validated the
+// arguments. mask_mode: 0 causal, 1 causal only when the prefix is non-empty, 2 no mask.
+pa_status launch_chunked_prefill_fp32(hipStream_t s, const pa_config* cfg, float* out, const void* q,
+                                      const int32_t* q_start_loc, const int32_t* prefix_lens, const float* k_cache,
+                                      const float* v_cache, const int32_t* block_tables, int32_t num_seqs,
+                                      int32_t max_blocks_per_seq, int32_t max_chunk_len, int32_t mask_mode);
 // Resolves the device address of pa_paged_decode_noalloc's scratch array on device `ordinal`
 // (paged_decode.hip); pa_device_open calls it once per device.
 pa_status init_decode_scratch(int ordinal);

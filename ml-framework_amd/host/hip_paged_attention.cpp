@@ -115,17 +115,6 @@ Tensor HipPagedAttentionKernel::ComputePagedAttention(const Tensor& query, const
                     vt[static_cast<size_t>(d) * 16 + r] = cachedValues.data[src + d];
                 }
             }
-    // One decode sequence per (batch, query); the reference's mask becomes its context length.
-    const int S = B * Q;
-    const bool masked = phase == AttentionPhase::Decode && C > Q;
-    std::vector<int32_t> lens(S), tables(static_cast<size_t>(S) * (nbb > 0 ? nbb : 1), -1);
-    for (int b = 0; b < B; b++)
-        for (int i = 0; i < Q; i++) {
-            const int s = b * Q + i;
-            lens[s] = masked ? C - Q + i + 1 : C;
-            for (int j = 0; j < nbb; j++) tables[static_cast<size_t>(s) * nbb + j] = b * nbb + j;
-        }
-
     pa_config cfg{};
     cfg.block_size = 16;
     cfg.num_q_heads = H;
@@ -136,17 +125,52 @@ Tensor HipPagedAttentionKernel::ComputePagedAttention(const Tensor& query, const
     cfg.num_blocks = nb;
     cfg.scale = scale > 0 ? scale : default_scale_;
     cfg.partition_size = 0;
-    cfg.flags = 0;
     const int mbps = nbb > 0 ? nbb : 1;
-    size_t wsb = 0;
-    check(pa_decode_workspace_size(&cfg, S, C, &wsb), "pa_decode_workspace_size");
-
     DeviceBuffer dq(device_, query.data.size() * 4), dk(device_, kc.size() * 4), dv(device_, vc.size() * 4),
-        dt(device_, tables.size() * 4), dl(device_, lens.size() * 4), dout(device_, out.data.size() * 4);
-    void* ws = wsb ? ensure_workspace(wsb) : nullptr;
+        dout(device_, out.data.size() * 4);
     check(pa_memcpy(dq.ptr, query.data.data(), query.data.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
     check(pa_memcpy(dk.ptr, kc.data(), kc.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
     check(pa_memcpy(dv.ptr, vc.data(), vc.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
+
+    if (Q > 1 && C >= Q) {
+        // Several queries over at least as many keys: one chunked-prefill launch in which the queries
+        // of a batch entry are its chunk, at positions C - Q .. C - 1. The reference masks only in the
+        // Decode phase and only when C > Q (StandardPagedAttentionKernel.cs:57-66): the literal mask
+        // rule, or no mask at all in the Prefill phase.
+        cfg.flags = phase == AttentionPhase::Decode ? PA_FLAG_REFERENCE_LITERAL_MASK : PA_FLAG_NO_MASK;
+        std::vector<int32_t> q_start(B + 1), prefix(B, C - Q), tables(static_cast<size_t>(B) * nbb);
+        for (int b = 0; b <= B; b++) q_start[b] = b * Q;
+        for (int b = 0; b < B; b++)
+            for (int j = 0; j < nbb; j++) tables[static_cast<size_t>(b) * nbb + j] = b * nbb + j;
+        DeviceBuffer dqs(device_, q_start.size() * 4), dp(device_, prefix.size() * 4), dt(device_, tables.size() * 4);
+        check(pa_memcpy(dqs.ptr, q_start.data(), q_start.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
+        check(pa_memcpy(dp.ptr, prefix.data(), prefix.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
+        check(pa_memcpy(dt.ptr, tables.data(), tables.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
+        check(pa_chunked_prefill(stream_, &cfg, static_cast<float*>(dout.ptr), dq.ptr,
+                                 static_cast<const int32_t*>(dqs.ptr), static_cast<const int32_t*>(dp.ptr), dk.ptr,
+                                 dv.ptr, nullptr, nullptr, static_cast<const int32_t*>(dt.ptr), B, mbps, Q),
+              "pa_chunked_prefill");
+        check(pa_memcpy(out.data.data(), dout.ptr, out.data.size() * 4, PA_MEMCPY_DEVICE_TO_HOST, stream_), "pa_memcpy");
+        check(pa_stream_synchronize(stream_), "pa_stream_synchronize");
+        return out;
+    }
+
+    // One query, or more queries than keys: one decode sequence per (batch, query), the reference's
+    // mask becoming its context length.
+    const int S = B * Q;
+    const bool masked = phase == AttentionPhase::Decode && C > Q;
+    std::vector<int32_t> lens(S), tables(static_cast<size_t>(S) * mbps, -1);
+    for (int b = 0; b < B; b++)
+        for (int i = 0; i < Q; i++) {
+            const int s = b * Q + i;
+            lens[s] = masked ? C - Q + i + 1 : C;
+            for (int j = 0; j < nbb; j++) tables[static_cast<size_t>(s) * mbps + j] = b * nbb + j;
+        }
+    cfg.flags = 0;
+    size_t wsb = 0;
+    check(pa_decode_workspace_size(&cfg, S, C, &wsb), "pa_decode_workspace_size");
+    DeviceBuffer dt(device_, tables.size() * 4), dl(device_, lens.size() * 4);
+    void* ws = wsb ? ensure_workspace(wsb) : nullptr;
     check(pa_memcpy(dt.ptr, tables.data(), tables.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
     check(pa_memcpy(dl.ptr, lens.data(), lens.size() * 4, PA_MEMCPY_HOST_TO_DEVICE, stream_), "pa_memcpy");
     check(pa_paged_decode(stream_, &cfg, static_cast<float*>(dout.ptr), dq.ptr, dk.ptr, dv.ptr, nullptr, nullptr,

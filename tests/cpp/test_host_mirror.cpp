@@ -231,6 +231,16 @@ static void gpu_tests() {
         dense_case(kern, 2, 20, 20, 8, 128, AttentionPhase::Prefill, -1.0f, 15, "prefill q=c=20");
         dense_case(kern, 1, 7, 50, 8, 128, AttentionPhase::Prefill, -1.0f, 16, "prefill q=7 c=50");
     });
+    run("LongPromptIsOneReadOnceLaunch", [&] {
+        // more than one query over at least as many keys runs as one chunked-prefill launch
+        dense_case(kern, 2, 512, 512, 8, 128, AttentionPhase::Prefill, -1.0f, 21, "prefill q=c=512");
+        dense_case(kern, 1, 512, 700, 8, 128, AttentionPhase::Decode, -1.0f, 22, "decode q=512 c=700");
+        dense_case(kern, 1, 512, 512, 4, 128, AttentionPhase::Decode, -1.0f, 23, "decode q=c=512");
+    });
+    run("MoreQueriesThanKeys", [&] {
+        dense_case(kern, 2, 20, 10, 4, 128, AttentionPhase::Decode, -1.0f, 24, "decode q=20 c=10");
+        dense_case(kern, 1, 9, 4, 4, 128, AttentionPhase::Prefill, -1.0f, 25, "prefill q=9 c=4");
+    });
     run("ExplicitScaleOverridesTheDefault", [&] {
         dense_case(kern, 2, 1, 64, 4, 128, AttentionPhase::Decode, 0.3f, 17, "scale 0.3");
     });
@@ -239,6 +249,8 @@ static void gpu_tests() {
         HipPagedAttentionKernel k64(64), k256(256);
         dense_case(k64, 2, 3, 33, 8, 64, AttentionPhase::Decode, -1.0f, 18, "D=64");
         dense_case(k256, 1, 1, 100, 2, 256, AttentionPhase::Decode, -1.0f, 19, "D=256");
+        dense_case(k64, 2, 40, 40, 4, 64, AttentionPhase::Prefill, -1.0f, 26, "D=64 prefill q=c=40");
+        dense_case(k256, 1, 33, 90, 2, 256, AttentionPhase::Decode, -1.0f, 27, "D=256 decode q=33 c=90");
     });
     run("UnsupportedHeadDimIsNotSupported", [&] {
         HipPagedAttentionKernel k48(48);

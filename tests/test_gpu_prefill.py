@@ -2,8 +2,8 @@
 
 The oracle gathers each sequence's prefix + chunk through its block table and runs the reference's
 StandardPagedAttentionKernel loops with the Decode-phase (bottom-right) mask
-(Kernels/StandardPagedAttentionKernel.cs:57-66, :219-255). Bar: (2e-3, 1e-2) for bf16 KV and
-(2e-2, 1e-2) for int8 KV, |gpu - oracle| <= atol + rtol*|oracle|.
+(Kernels/StandardPagedAttentionKernel.cs:57-66, :219-255). Bar: (1e-5, 1e-4) for fp32 KV,
+(2e-3, 1e-2) for bf16 KV and (2e-2, 1e-2) for int8 KV, |gpu - oracle| <= atol + rtol*|oracle|.
 """
 import os
 
@@ -80,6 +80,33 @@ def test_prefill_ragged(stream, flags, kv_dtype, q_dtype, Hq, Hkv, D):
     got, ref = run_prefill(stream, prefix=PREFIX, chunk=CHUNK, Hq=Hq, Hkv=Hkv, D=D, kv_dtype=kv_dtype,
                            q_dtype=q_dtype, flags=flags, seed=D + kv_dtype)
     check_close(got, ref, **tol_for(kv_dtype), what=f"prefill flags={flags} kv={kv_dtype} D={D} G={Hq // Hkv}")
+
+
+@pytest.mark.parametrize("flags", [0, pa.PA_FLAG_REFERENCE_LITERAL_MASK, pa.PA_FLAG_NO_MASK])
+@pytest.mark.parametrize("q_dtype,Hq,Hkv,D", [(0, 8, 8, 128), (1, 16, 4, 64), (0, 8, 2, 32), (0, 4, 1, 256)])
+def test_prefill_fp32_cache(stream, flags, q_dtype, Hq, Hkv, D):
+    """fp32 caches through the fp32 prefill kernel (fp32 operands and accumulation), held to the
+    fp32 bar over ragged chunks, scattered block tables and every mask mode."""
+    got, ref = run_prefill(stream, prefix=PREFIX, chunk=CHUNK, Hq=Hq, Hkv=Hkv, D=D, kv_dtype=0, q_dtype=q_dtype,
+                           flags=flags, seed=D + Hq)
+    check_close(got, ref, **tol_for(0), what=f"fp32 prefill flags={flags} D={D} G={Hq // Hkv}")
+
+
+def test_prefill_fp32_long_prompt(stream):
+    """A 512-query prompt after a 700-token prefix and a whole 512-token prompt, fp32 cache."""
+    got, ref = run_prefill(stream, prefix=[700, 0], chunk=[512, 512], Hq=8, Hkv=8, D=128, kv_dtype=0, q_dtype=0,
+                           seed=21)
+    check_close(got, ref, **tol_for(0), what="fp32 512-query prefill")
+
+
+def test_prefill_fp32_invalid_block_ids_read_as_zero(stream):
+    def edit(w):
+        w.block_tables[0, 1] = -1
+        w.block_tables[1, 3] = w.num_blocks + 5
+
+    got, ref = run_prefill(stream, prefix=[40, 20], chunk=[30, 50], Hq=8, Hkv=2, D=64, kv_dtype=0, q_dtype=0,
+                           seed=22, table_edit=edit)
+    check_close(got, ref, **tol_for(0), what="fp32 invalid ids")
 
 
 def test_prefill_empty_chunks_and_single_query(stream):
