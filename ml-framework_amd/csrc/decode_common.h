@@ -154,6 +154,13 @@ __device__ __forceinline__ uint32_t pack_bf16_trunc(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
+// fp32 -> bf16 bits rounded to nearest even, two at a time (gfx950's v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ uint32_t pack_i8pair(uint32_t w, int k) {
     // Codes k and k+1 of w as two bf16 (exact: |code| <= 128 needs 8 significant bits).
     return pack_bf16_trunc(pa::i8_at(w, k), pa::i8_at(w, k + 1));

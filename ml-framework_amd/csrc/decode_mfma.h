@@ -321,7 +321,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     // k_dim0(2t, q4) .. +16, i.e. K registers 2t and 2t + 1.
     constexpr int NI8 = NSLAB / 2;
     i32x4_t qdh[KV == PA_DTYPE_INT8 ? NI8 : 1], qdl[KV == PA_DTYPE_INT8 ? NI8 : 1];
-    float q_sq = 0.0f;
+    float q_sq_scaled = 0.0f;  // q_sq times the softmax scale
     auto int8_q_digits = [&](const float (&x)[NSLAB][8]) {
         float mx = 0.0f;
 #pragma unroll
@@ -329,7 +329,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
 #pragma unroll
             for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(x[sl][e]));
         mx = rows_max(mx);  // max |q| of head n
-        q_sq = mx * (1.0f / 32639.0f);
+        q_sq_scaled = mx * (1.0f / 32639.0f) * a.scale;
         const float inv = mx > 0.0f ? 32639.0f / mx : 0.0f;
 #pragma unroll
         for (int t = 0; t < NI8; t++) {
@@ -471,14 +471,17 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                 if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[sl], s, 0, 0, 0);
             }
         }
-        const int tbase = (g.b0 + e) * 16 + 4 * q4;
+        // int8: (Q16 . code) times q_sq k_scale scale, one factor per block and head
+        const float sf = KV == PA_DTYPE_INT8 ? ks * q_sq_scaled : a.scale;
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v = s[i];
-            if constexpr (KV == PA_DTYPE_INT8) v = v * (ks * q_sq);  // (Q16 . code) q_sq k_scale, then * scale
-            v = v * a.scale;
-            sc[i] = tbase + i < T ? v : -INFINITY;
+        for (int i = 0; i < 4; i++) sc[i] = s[i] * sf;
+        // only a row's last block can hold tokens past T (a uniform test: no per-score compare
+        // on the others)
+        if ((g.b0 + e + 1) * 16 > T) {
+            const int lim = T - ((g.b0 + e) * 16 + 4 * q4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) sc[i] = i < lim ? sc[i] : -INFINITY;
         }
         const float bm = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
         const bool grow = bm > m_run + kRescaleThreshold;
@@ -503,15 +506,11 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
         }
         if constexpr (KV == PA_DTYPE_INT8) {
-            // int8 caches (bar 2e-2): one bf16 P, rounded to nearest (relative error <= 2^-9),
-            // half the PV MFMAs of the split below. p is finite and non-negative.
+            // int8 caches (bar 2e-2): one bf16 P, rounded to nearest even (relative error <= 2^-9;
+            // v_cvt_pk_bf16_f32), half the PV MFMAs of the split below. p is finite and non-negative.
             uint32_t pr[2];
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const uint32_t b0 = __float_as_uint(p[2 * e]), b1 = __float_as_uint(p[2 * e + 1]);
-                pr[e] = pack_bf16_trunc(__uint_as_float(b0 + 0x7fffu + ((b0 >> 16) & 1u)),
-                                        __uint_as_float(b1 + 0x7fffu + ((b1 >> 16) & 1u)));
-            }
+            for (int e = 0; e < 2; e++) pr[e] = pack_bf16_rne(p[2 * e], p[2 * e + 1]);
             const s16x4_t pb = __builtin_bit_cast(s16x4_t, make_uint2(pr[0], pr[1]));
 #pragma unroll
             for (int t = 0; t < NT; t++)
