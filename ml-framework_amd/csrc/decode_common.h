@@ -92,7 +92,8 @@ __device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
 // The new token (position T - 1 of sequence seq, KV head kvh; T = its clamped context length >= 2)
 // written into a bf16 cache as pa_kv_append stores it: K row (T - 1) % 16 and V column (T - 1) % 16
 // of the block the table gives for it, bf16 by truncation. One wave, lane l takes dims l, l + 64, ..
-// Written by the merge kernel, after the decode's streaming, with non-temporal stores: the V column
+// Written by the merge kernel's fifth wave (beside the four merging ones, so its round trip is not
+// added to theirs), after the decode's streaming, with non-temporal stores: the V column
 // touches one line per two dims of the transposed tile, and written among the decode's reads, or
 // left dirty in the caches for the next step's reads to evict, those lines cost the C2 step 3-4 us
 // (measured: in the decode, in the merge kernel with plain stores, as whole tiles read and
@@ -327,10 +328,17 @@ __device__ __forceinline__ int64_t split_range_blocks(const DecodeArgs& a, int64
 // R0 + nbr - 1 fall in different ranges, and then ranges w1 .. w2 each left one partial per KV
 // head, in unit u = w * Hkv + kvh: slot 2u, except range w1 when the sequence starts inside it (the
 // row is then that unit's last row portion, slot 2u + 1).
+// Launched with kMergeThreads threads, or kMergeThreads + 64 when it also writes the fused
+// append's token (a.append_in_merge): that fifth wave only writes the token.
+constexpr int kMergeThreads = 256;
 template <int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_split_kernel(const DecodeArgs a, int32_t num_seqs) {
+__global__ __launch_bounds__(kMergeThreads + 64) void paged_decode_merge_split_kernel(const DecodeArgs a,
+                                                                                      int32_t num_seqs) {
     const int kvh = blockIdx.x, seq = blockIdx.y;
-    if (a.append_in_merge && threadIdx.x >= 192) append_token_bf16<D>(a, seq, kvh);  // the last wave
+    if (threadIdx.x >= kMergeThreads) {
+        if (a.append_in_merge) append_token_bf16<D>(a, seq, kvh);
+        return;
+    }
     const int64_t R0 = a.ws_pref[seq];
     const int nbr = a.ws_pref[seq + 1] - a.ws_pref[seq];
     const int64_t total = a.ws_pref[num_seqs];

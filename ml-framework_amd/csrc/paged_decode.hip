@@ -350,11 +350,12 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
     PA_HIP_CHECK(hipGetLastError());
     if (merge) {
         dim3 mgrid(cfg->num_kv_heads, num_seqs);
+        const int mthreads = pa::kMergeThreads + (a.append_in_merge ? 64 : 0);
         switch (cfg->head_dim) {
-            case 32: pa::paged_decode_merge_split_kernel<32><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
-            case 64: pa::paged_decode_merge_split_kernel<64><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
-            case 128: pa::paged_decode_merge_split_kernel<128><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
-            default: pa::paged_decode_merge_split_kernel<256><<<mgrid, 256, 0, s>>>(a, num_seqs); break;
+            case 32: pa::paged_decode_merge_split_kernel<32><<<mgrid, mthreads, 0, s>>>(a, num_seqs); break;
+            case 64: pa::paged_decode_merge_split_kernel<64><<<mgrid, mthreads, 0, s>>>(a, num_seqs); break;
+            case 128: pa::paged_decode_merge_split_kernel<128><<<mgrid, mthreads, 0, s>>>(a, num_seqs); break;
+            default: pa::paged_decode_merge_split_kernel<256><<<mgrid, mthreads, 0, s>>>(a, num_seqs); break;
         }
         PA_HIP_CHECK(hipGetLastError());
     }
