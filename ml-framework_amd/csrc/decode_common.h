@@ -30,7 +30,6 @@ struct DecodeArgs {
     float* ws_m;  // [rows]
     float* ws_l;  // [rows]
     int32_t* ws_pref;  // MFMA kernel: [num_seqs + 1] blocks per KV-head row before each sequence
-    int32_t* ws_abid;  // MFMA kernel, fused bf16 append: [num_seqs][Hkv] the new token's block id
     // fused append (pa_paged_decode_append): the token at position context_len - 1
     const void* k_new;  // [num_seqs][Hkv][D] of the activation dtype
     const void* v_new;
@@ -100,10 +99,10 @@ __device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
 // rewritten; non-temporal 2-byte stores here cost the least).
 template <int D>
 __device__ __forceinline__ void append_token_bf16(const DecodeArgs& a, int seq, int kvh) {
-    // One round trip: the length, the block id the decode left in the workspace, the values.
+    // The length, then the table entry of the token's block (the values' loads go out with it).
     const int T = clamp_len(a, a.context_lens[seq]);
-    const int bid = a.ws_abid[static_cast<int64_t>(seq) * a.num_kv_heads + kvh];
     if (T < 2) return;  // T == 1: the decode writes it (no streamed block); T <= 0: nothing
+    const int bid = a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + (T - 1) / 16];
     if (bid < 0 || bid >= a.num_blocks) return;
     const int lane = threadIdx.x & 63, r = (T - 1) & 15;
     const bool f32 = !a.q_bf16;

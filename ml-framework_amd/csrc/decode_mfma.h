@@ -543,7 +543,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
     int abid = -1;
     auto prefetch_vtile = [&]() {
         if constexpr (APPEND) {
-            if (piece_owns_new<APPEND>(g)) {
+            if (piece_owns_new<APPEND>(g) && !a.append_in_merge) {
                 if ((T & 15) != 0) {
                     abid = __builtin_amdgcn_readlane(my_bid, nb - 1);
                 } else if (nb < kPieceBlocks) {
@@ -555,10 +555,6 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
                         a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + T / 16 + zero]);
                 }
                 abid = valid_bid(a, abid);
-                if (a.append_in_merge) {  // the merge kernel writes the token at block abid
-                    if (lane == 0) a.ws_abid[static_cast<int64_t>(seq) * Hkv + kvh] = abid;
-                    return;
-                }
                 constexpr uint32_t kTileBytes = TILE * 2;
                 const int64_t tile = abid >= 0 ? (static_cast<int64_t>(abid) * Hkv + kvh) * kTileBytes : 0;
                 const u32x4_t rv = buffer_rsrc_words(static_cast<const char*>(a.v_cache) + tile,

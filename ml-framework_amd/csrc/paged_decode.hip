@@ -102,9 +102,8 @@ size_t workspace_bytes_for(const pa_config* cfg, int32_t num_seqs, int32_t max_l
     }
     const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
     const int64_t rows = 2 * mfma_max_units(cfg, num_seqs, max_len, part, cfg->num_splits) * (cfg->num_q_heads / cfg->num_kv_heads);
-    // partials (o, max, sum), sequence offsets, the fused append's block ids
-    return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float) + static_cast<size_t>(seqs + 1) * 4 +
-           static_cast<size_t>(seqs) * cfg->num_kv_heads * 4;
+    // partials (o, max, sum), sequence offsets
+    return static_cast<size_t>(rows) * (cfg->head_dim + 2) * sizeof(float) + static_cast<size_t>(seqs + 1) * 4;
 }
 
 int32_t effective_max_len(int32_t max_context_len, int32_t max_blocks_per_seq) {
@@ -300,10 +299,6 @@ pa_status decode_chunk(const char* fn, bool append, pa_stream* stream, const pa_
         a.ws_m = a.ws_o + rows * cfg->head_dim;
         a.ws_l = a.ws_m + rows;
         a.ws_pref = reinterpret_cast<int32_t*>(a.ws_l + rows);
-        if (!fp32) {
-            const int64_t seqs = num_seqs < pa::kMaxPersistentSeqs - 1 ? num_seqs : pa::kMaxPersistentSeqs - 1;
-            a.ws_abid = a.ws_pref + seqs + 1;
-        }
     }
 
     hipStream_t s = pa::native(stream);

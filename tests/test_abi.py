@@ -109,16 +109,15 @@ def test_workspace_size():
     c = cfg()  # Hq 32, Hkv 8, D 128, bf16
     # bf16/int8, default split: 2 partial slots per unit (range, KV head) of (D + 2) floats per query
     # head of the group (G = 4); ranges <= min(4096 workers / Hkv, ceil(blocks / 4)) where blocks
-    # counts one KV head; plus num_seqs + 1 ints of sequence offsets and num_seqs x Hkv ints of the
-    # fused append's block ids.
+    # counts one KV head; plus num_seqs + 1 ints of sequence offsets.
     # 64 x 4096 tokens = 16384 blocks -> min(512, 4096) = 512 ranges x 8 KV heads
-    assert pa.decode_workspace_size(c, 64, 4096) == 2 * 4096 * 4 * 130 * 4 + 65 * 4 + 64 * 8 * 4
+    assert pa.decode_workspace_size(c, 64, 4096) == 2 * 4096 * 4 * 130 * 4 + 65 * 4
     # 1 sequence of 16 tokens: 1 block -> 1 range x 8 KV heads
-    assert pa.decode_workspace_size(c, 1, 16) == 2 * 8 * 4 * 130 * 4 + 2 * 4 + 8 * 4
+    assert pa.decode_workspace_size(c, 1, 16) == 2 * 8 * 4 * 130 * 4 + 2 * 4
     # fixed 512-token ranges (32 blocks): 16384 / 32 = 512 ranges x 8 KV heads
-    assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 2 * 4096 * 4 * 130 * 4 + 65 * 4 + 64 * 8 * 4
+    assert pa.decode_workspace_size(cfg(partition_size=512), 64, 4096) == 2 * 4096 * 4 * 130 * 4 + 65 * 4
     # beyond one launch's 2047 sequences the launches reuse the workspace: sized for 2047
-    assert pa.decode_workspace_size(c, 5000, 64) == 2 * 4096 * 4 * 130 * 4 + 2048 * 4 + 2047 * 8 * 4
+    assert pa.decode_workspace_size(c, 5000, 64) == 2 * 4096 * 4 * 130 * 4 + 2048 * 4
     assert pa.decode_workspace_size(c, 0, 4096) == 0
     # fp32: per-partition partials only when some sequence needs more than one partition
     assert pa.decode_workspace_size(cfg(kv_dtype=0), 4, 256) == 0
@@ -129,8 +128,8 @@ def test_workspace_size():
     with pytest.raises(pa.PagedAttentionError):
         pa.decode_workspace_size(cfg(kv_dtype=0, partition_size=1024), 4, 256)
     # per-sequence split P: P units per (sequence, KV head), 2 slots each
-    assert pa.decode_workspace_size(cfg(num_splits=16), 8, 32768) == 2 * 8 * 16 * 8 * 4 * 130 * 4 + 9 * 4 + 8 * 8 * 4
-    assert pa.decode_workspace_size(cfg(num_splits=1), 3, 100) == 2 * 3 * 8 * 4 * 130 * 4 + 4 * 4 + 3 * 8 * 4
+    assert pa.decode_workspace_size(cfg(num_splits=16), 8, 32768) == 2 * 8 * 16 * 8 * 4 * 130 * 4 + 9 * 4
+    assert pa.decode_workspace_size(cfg(num_splits=1), 3, 100) == 2 * 3 * 8 * 4 * 130 * 4 + 4 * 4
     for bad in (dict(num_splits=-1), dict(num_splits=257), dict(num_splits=4, partition_size=512),
                 dict(num_splits=4, kv_dtype=0)):
         with pytest.raises(pa.PagedAttentionError) as e:
