@@ -105,6 +105,27 @@ def test_argument_validation():
     pa.kv_append(None, c, None, None, None, 0, None, None)
 
 
+@pytest.mark.parametrize("c,args,status,msg", [
+    (cfg(), (-1, 4, 16), pa.PA_ERROR_INVALID_ARGUMENT, "negative"),
+    (cfg(), (70000, 4, 16), pa.PA_ERROR_UNSUPPORTED, "65535"),
+    (cfg(), (2, 0, 16), pa.PA_ERROR_INVALID_ARGUMENT, "block"),
+    (cfg(flags=pa.PA_FLAG_REFERENCE_LITERAL_MASK | pa.PA_FLAG_NO_MASK), (2, 4, 16), pa.PA_ERROR_INVALID_CONFIG,
+     "mask"),
+    (cfg(head_dim=32), (2, 4, 16), pa.PA_ERROR_UNSUPPORTED, "head_dim"),
+    (cfg(kv_dtype=pa.PA_DTYPE_INT8), (2, 4, 16), pa.PA_ERROR_INVALID_ARGUMENT, "k_scale"),
+])
+def test_prefill_argument_validation(c, args, status, msg):
+    with pytest.raises(pa.PagedAttentionError) as e:
+        pa.chunked_prefill(None, c, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, FAKE, *args)
+    assert e.value.status == status and msg in str(e.value)
+    with pytest.raises(pa.PagedAttentionError) as e:  # null block table
+        pa.chunked_prefill(None, cfg(), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None, 2, 4, 16)
+    assert e.value.status == pa.PA_ERROR_INVALID_ARGUMENT
+    # no sequences or no queries: a no-op that touches no pointer
+    pa.chunked_prefill(None, cfg(), None, None, None, None, None, None, None, None, None, 0, 4, 16)
+    pa.chunked_prefill(None, cfg(), None, None, None, None, None, None, None, None, None, 2, 4, 0)
+
+
 def test_workspace_size():
     c = cfg()  # Hq 32, Hkv 8, D 128, bf16
     # bf16/int8, default split: 2 partial slots per unit (range, KV head) of (D + 2) floats per query
