@@ -15,10 +15,11 @@
 //
 // A portion is streamed in pieces of at most 64 blocks (lane j holds the id of the piece's block
 // j); the running (max, sum, O) carry over from piece to piece and are written when the portion
-// ends. Block ids are loaded two pieces ahead. Kernels with bf16 queries and head_dim <= 128 also
-// carry the pipeline across pieces: a piece issues the next one's Q and scales at its start and
-// its first two blocks in its last two iterations, so a piece or row boundary does not drain the
-// blocks in flight. The others start a piece with its own loads (one memory round trip).
+// ends. Block ids are loaded two pieces ahead. Kernels with head_dim <= 128 and bf16 queries or
+// int8 caches also carry the pipeline across pieces: a piece issues the next one's Q and scales at
+// its start and its first two blocks in its last two iterations, so a piece or row boundary does
+// not drain the blocks in flight. The others start a piece with its own loads (one memory round
+// trip).
 //
 // Fused append (pa_paged_decode_append, bf16 caches): a row streams its first T - 1 cached tokens
 // only; the new token (position T - 1, from k_new / v_new) joins the softmax as one more element at
@@ -132,7 +133,7 @@ struct PipeBufs {
 // Vector memory instructions load_block issues per block.
 template <int D, int KV>
 __host__ __device__ constexpr int decode_block_loads() {
-    return (KV == PA_DTYPE_INT8 ? D / 64 : D / 32) + D / 16;
+    return KV == PA_DTYPE_INT8 ? D / 64 + (D >= 64 ? D / 64 : D / 16) : D / 32 + D / 16;
 }
 // s_waitcnt operand: wait until at most N vector memory operations are outstanding (no wait on
 // the other counters).
@@ -142,11 +143,12 @@ __host__ __device__ constexpr int vmcnt_keep() {
     return (N & 15) | 0x7 << 4 | 0xf << 8 | (N >> 4) << 14;
 }
 
-// Carry across pieces (bf16 queries, head_dim <= 128): elsewhere the extra registers (the next
-// piece's Q) would spill, so those kernels start every piece with its own loads.
+// Carry across pieces (head_dim <= 128 with bf16 queries, or with int8 caches, whose K/V buffers
+// are half the size): elsewhere the extra registers (the next piece's Q) would spill, so those
+// kernels start every piece with its own loads.
 template <int D, int KV, bool QF32, bool APPEND>
 __host__ __device__ constexpr bool decode_carry() {
-    return decode_buffers(KV) == 3 && !QF32 && D <= 128;
+    return decode_buffers(KV) == 3 && (!QF32 || KV == PA_DTYPE_INT8) && D <= 128;
 }
 
 // Leading empty iterations of a carried piece of nb blocks: its iteration count nb + lead is a
@@ -227,8 +229,15 @@ __device__ __forceinline__ void load_side(const DecodeArgs& a, const Piece& g, i
     }
 }
 
+// int8 caches with D >= 64 load V 16 bytes per lane (int8_v_transpose).
+template <int D, int KV>
+__host__ __device__ constexpr bool int8_wide_v() {
+    return KV == PA_DTYPE_INT8 && D >= 64;
+}
+
 // Loads of block bid (K/V tile of KV head kv) into a pipeline buffer, lane (q4, n): K row n (the
-// lane's dims of each slab), V dim n of tokens 4q4 .. 4q4 + 3 (every 16th dim). Loads go through
+// lane's dims of each slab), V dim n of tokens 4q4 .. 4q4 + 3 (every 16th dim; int8 with D >= 64:
+// 16-byte loads whose words int8_v_transpose() puts in that order). Loads go through
 // per-block buffer descriptors: bid < 0 (past a list, or an invalid id) gives a zero-sized
 // descriptor, so its loads return zeros without touching memory. The load sequence is therefore
 // identical on every iteration (no branches), which lets the compiler wait for exactly the oldest
@@ -265,8 +274,38 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
 #pragma unroll
         for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kCPK>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
     }
+    if constexpr (int8_wide_v<D, KV>()) {
+        // int8, D >= 64: load u of lane (q4, n) is all 16 tokens of dim 16 (q4 + 4u) + n (one
+        // contiguous KiB per instruction, a quarter of the instructions of 4-byte loads);
+        // int8_v_transpose() turns words vr[4u .. 4u + 3] into tiles 4u .. 4u + 3.
 #pragma unroll
-    for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kCPV>(rv, v_lane_off + 256 * t * ELT);
+        for (int u = 0; u < D / 64; u++) {
+            const uint4 w = buffer_load<uint4, kCPV>(rv, (16 * (q4 + 4 * u) + n) * 16);
+            vr[4 * u] = w.x;
+            vr[4 * u + 1] = w.y;
+            vr[4 * u + 2] = w.z;
+            vr[4 * u + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kCPV>(rv, v_lane_off + 256 * t * ELT);
+    }
+}
+
+// int8 V words after a wide load: lane (q4, n) holds, in w[k], tokens 4k .. 4k + 3 of dim
+// 16 (q4 + 4u) + n. The PV MFMA of tile 4u + t needs tokens 4 q4 .. 4 q4 + 3 of dim 16 (4u + t) + n
+// in lane (q4, n): word q4 of row group t, i.e. a 4 x 4 transpose of words across the four rows of
+// 16 lanes. v_permlane32_swap exchanges rows 2, 3 of its first operand with rows 0, 1 of its second,
+// v_permlane16_swap the odd rows of the first with the even rows of the second.
+__device__ __forceinline__ void int8_v_transpose(uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3) {
+    const auto a = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    w0 = c[0];
+    w1 = c[1];
+    w2 = d[0];
+    w3 = d[1];
 }
 
 // One piece, streamed by one wave; my_bid = piece_ids(..). has_next, nxt, nxt_ids: the next piece
@@ -506,6 +545,10 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
         }
         if constexpr (KV == PA_DTYPE_INT8) {
+            if constexpr (int8_wide_v<D, KV>()) {
+#pragma unroll
+                for (int u = 0; u < D / 64; u++) int8_v_transpose(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
+            }
             // int8 caches (bar 2e-2): one bf16 P, rounded to nearest even (relative error <= 2^-9;
             // v_cvt_pk_bf16_f32), half the PV MFMAs of the split below. p is finite and non-negative.
             uint32_t pr[2];
