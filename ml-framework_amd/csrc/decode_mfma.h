@@ -133,7 +133,7 @@ struct PipeBufs {
 // Vector memory instructions load_block issues per block.
 template <int D, int KV>
 __host__ __device__ constexpr int decode_block_loads() {
-    return KV == PA_DTYPE_INT8 ? D / 64 + (D >= 64 ? D / 64 : D / 16) : D / 32 + D / 16;
+    return KV == PA_DTYPE_INT8 ? D / 64 + (D >= 64 ? D / 64 : D / 16) : D / 32 + D / 32;
 }
 // s_waitcnt operand: wait until at most N vector memory operations are outstanding (no wait on
 // the other counters).
@@ -235,9 +235,18 @@ __host__ __device__ constexpr bool int8_wide_v() {
     return KV == PA_DTYPE_INT8 && D >= 64;
 }
 
+// Tokens 4 tok_group(q4) .. + 3 of a block are the QK MFMA rows (S^T) and PV MFMA k values of lane
+// group q4. bf16 caches exchange groups 1 and 2 (bf16_v_exchange), so their K rows are loaded in
+// that order as well.
+template <int KV>
+__device__ __forceinline__ int tok_group(int q4) {
+    return KV == PA_DTYPE_BF16 ? ((q4 & 1) << 1) | (q4 >> 1) : q4;
+}
+
 // Loads of block bid (K/V tile of KV head kv) into a pipeline buffer, lane (q4, n): K row n (the
-// lane's dims of each slab), V dim n of tokens 4q4 .. 4q4 + 3 (every 16th dim; int8 with D >= 64:
-// 16-byte loads whose words int8_v_transpose() puts in that order). Loads go through
+// lane's dims of each slab; bf16: row 4 tok_group(n / 4) + n % 4), V dim n of tokens 4q4 .. 4q4 + 3
+// (every 16th dim; bf16 and int8 with D >= 64: 16-byte loads whose words bf16_v_exchange() /
+// int8_v_transpose() put in that order, bf16 with tok_group). Loads go through
 // per-block buffer descriptors: bid < 0 (past a list, or an invalid id) gives a zero-sized
 // descriptor, so its loads return zeros without touching memory. The load sequence is therefore
 // identical on every iteration (no branches), which lets the compiler wait for exactly the oldest
@@ -255,7 +264,8 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
     constexpr int kCPV = kLoadNonTemporal;
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4, n = lane & 15;
-    const int k_row_off = n * D * ELT;               // K row n; slab s of this lane starts at dim k_dim0(s, q4)
+    const int krow = KV == PA_DTYPE_BF16 ? 4 * tok_group<KV>(n >> 2) + (n & 3) : n;
+    const int k_row_off = krow * D * ELT;            // K row krow; slab s of this lane starts at dim k_dim0(s, q4)
     const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
     const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * a.num_kv_heads + kv) * TILE * ELT : 0;
     const int bytes = bid >= 0 ? TILE * ELT : 0;
@@ -274,7 +284,17 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
 #pragma unroll
         for (int s = 0; s < NSLAB; s++) kr[s] = buffer_load<KR, kCPK>(rk, k_row_off + k_dim0<D, KV>(s, q4) * ELT);
     }
-    if constexpr (int8_wide_v<D, KV>()) {
+    if constexpr (KV == PA_DTYPE_BF16) {
+        // bf16: load u of lane (q4, n) is tokens 8 (q4 % 2) .. + 7 of dim 32u + 16 (q4 / 2) + n
+        // (one contiguous KiB per instruction, two tiles: half the instructions of 8-byte loads);
+        // bf16_v_exchange() turns vr[2u], vr[2u + 1] into tiles 2u, 2u + 1.
+#pragma unroll
+        for (int u = 0; u < D / 32; u++) {
+            const uint4 w = buffer_load<uint4, kCPV>(rv, (32 * u + 16 * (q4 >> 1) + n) * 32 + 16 * (q4 & 1));
+            vr[2 * u] = make_uint2(w.x, w.y);
+            vr[2 * u + 1] = make_uint2(w.z, w.w);
+        }
+    } else if constexpr (int8_wide_v<D, KV>()) {
         // int8, D >= 64: load u of lane (q4, n) is all 16 tokens of dim 16 (q4 + 4u) + n (one
         // contiguous KiB per instruction, a quarter of the instructions of 4-byte loads);
         // int8_v_transpose() turns words vr[4u .. 4u + 3] into tiles 4u .. 4u + 3.
@@ -306,6 +326,17 @@ __device__ __forceinline__ void int8_v_transpose(uint32_t& w0, uint32_t& w1, uin
     w1 = c[1];
     w2 = d[0];
     w3 = d[1];
+}
+
+// bf16 V after a wide load: lane group q4 holds, in (x0, x1), tokens 8 (q4 % 2) .. + 3 and
+// 8 (q4 % 2) + 4 .. + 7 of tile 2u (q4 < 2) or 2u + 1 (q4 >= 2). One exchange of rows 2, 3 of x0
+// with rows 0, 1 of x1 (per 32-bit word) leaves tile 2u in x0 and tile 2u + 1 in x1, each with
+// tokens 4 tok_group(q4) .. + 3 in lane group q4 (groups 1 and 2 exchanged).
+__device__ __forceinline__ void bf16_v_exchange(uint2& x0, uint2& x1) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x0.x, x1.x, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x0.y, x1.y, false, false);
+    x0 = make_uint2(a[0], b[0]);
+    x1 = make_uint2(a[1], b[1]);
 }
 
 // One piece, streamed by one wave; my_bid = piece_ids(..). has_next, nxt, nxt_ids: the next piece
@@ -488,7 +519,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             ks = bid >= 0 ? readlane_f(side.ks, e) : 0.0f;
             vfac = bid >= 0 ? readlane_f(side.vs, e) : 0.0f;
         }
-        // S^T[token 4q4+i][head n]
+        // S^T[token 4 tok_group(q4) + i][head n]
         f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (KV == PA_DTYPE_INT8) {
             i32x4_t ch = {0, 0, 0, 0}, cl = {0, 0, 0, 0};
@@ -518,7 +549,7 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
         // only a row's last block can hold tokens past T (a uniform test: no per-score compare
         // on the others)
         if ((g.b0 + e + 1) * 16 > T) {
-            const int lim = T - ((g.b0 + e) * 16 + 4 * q4);
+            const int lim = T - ((g.b0 + e) * 16 + 4 * tok_group<KV>(q4));
 #pragma unroll
             for (int i = 0; i < 4; i++) sc[i] = i < lim ? sc[i] : -INFINITY;
         }
@@ -559,6 +590,8 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             for (int t = 0; t < NT; t++)
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pb, v_operand(vr[t]), acc[t], 0, 0, 0);
         } else {
+#pragma unroll
+            for (int u = 0; u < D / 32; u++) bf16_v_exchange(vr[2 * u], vr[2 * u + 1]);
             uint32_t hi[2], lo[2];
 #pragma unroll
             for (int e = 0; e < 2; e++) {
