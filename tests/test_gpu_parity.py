@@ -446,6 +446,21 @@ def test_decode_num_splits(stream, nsp, kv_dtype, q_dtype, Hq, Hkv, D):
     assert np.all(got[0] == 0.0)
 
 
+@pytest.mark.parametrize("part", [0, 64])
+@pytest.mark.parametrize("kv_dtype,q_dtype,Hq,Hkv,D", [(1, 1, 32, 8, 128), (1, 0, 8, 2, 64), (1, 1, 16, 4, 256),
+                                                        (2, 0, 32, 8, 128), (2, 1, 8, 8, 64)])
+def test_decode_every_tail_position(stream, part, kv_dtype, q_dtype, Hq, Hkv, D):
+    """A row's last block holding 1 to 16 tokens, each in a row of its own (and rows of one to three
+    blocks). The kernels hand a lane group four consecutive tokens of a block (the bf16 kernel
+    with groups 1 and 2 exchanged, so its K rows and the tail mask follow the same numbering), so
+    every count of tokens in the last block masks a different set of lanes."""
+    lens = [16 * b + r for b in (0, 1, 2) for r in range(1, 17)]
+    w = wl.make_small(500 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
+                      kv_dtype=kv_dtype, q_dtype=q_dtype)
+    got, ref = run_decode(w, 63, stream, partition_size=part)
+    check_close(got, ref, **tol_for(kv_dtype), what=f"tail positions kv={kv_dtype} D={D} part={part}")
+
+
 def test_decode_invalid_block_ids_read_as_zero(stream):
     w = wl.make_small(9, num_seqs=4, lens=[40, 300, 700, 33], Hq=16, Hkv=4, D=128, kv_dtype=1, q_dtype=1)
     w.block_tables[1, 3] = -1
@@ -457,6 +472,7 @@ def test_decode_invalid_block_ids_read_as_zero(stream):
 # ---- fused append + decode ------------------------------------------------------------------------
 # Positions T-1 with (T-1) % 16 == 0 start a block (fresh int8 statistics); the rest append mid-block.
 APPEND_LENS = [1, 2, 16, 17, 33, 100, 256, 257, 300, 513, 1000, 1024, 1025, 2000]
+TAIL_LENS = [16 * b + r for b in (0, 1, 2) for r in range(1, 17)]  # every position of the new token
 
 
 # Long rows: segments of up to 256 blocks (64 per wave), the appended block at a late lane;
@@ -469,8 +485,9 @@ LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000, 1025, 2049]
     (1, 1, 32, 8, 128, 0, APPEND_LENS), (1, 0, 16, 4, 64, 512, APPEND_LENS), (2, 0, 32, 8, 128, 0, APPEND_LENS),
     (2, 1, 8, 2, 256, 512, APPEND_LENS), (0, 0, 8, 8, 64, 256, APPEND_LENS), (0, 1, 16, 4, 128, 512, APPEND_LENS),
     (1, 1, 16, 4, 128, 256, APPEND_LENS), (1, 1, 8, 2, 128, 4096, LONG_LENS), (2, 1, 8, 2, 128, 0, LONG_LENS),
+    (1, 1, 32, 8, 128, 0, TAIL_LENS), (2, 0, 32, 8, 128, 0, TAIL_LENS),
 ], ids=["bf16-split16", "int8-split5", "bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
-        "int8-long"])
+        "int8-long", "bf16-tails", "int8-tails"])
 def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part, lens):
     w = wl.make_small(70 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
                       kv_dtype=kv_dtype, q_dtype=q_dtype)
