@@ -486,8 +486,11 @@ LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000, 1025, 2049]
     (2, 1, 8, 2, 256, 512, APPEND_LENS), (0, 0, 8, 8, 64, 256, APPEND_LENS), (0, 1, 16, 4, 128, 512, APPEND_LENS),
     (1, 1, 16, 4, 128, 256, APPEND_LENS), (1, 1, 8, 2, 128, 4096, LONG_LENS), (2, 1, 8, 2, 128, 0, LONG_LENS),
     (1, 1, 32, 8, 128, 0, TAIL_LENS), (2, 0, 32, 8, 128, 0, TAIL_LENS),
+    # one range, no merge launch: the owning wave writes the token (V tile patched in LDS)
+    (1, 1, 32, 8, 128, 0, [40]), (1, 0, 8, 2, 64, -1, [1000]), (1, 1, 8, 2, 128, -1, [33]), (1, 1, 16, 4, 256, 0, [64]),
 ], ids=["bf16-split16", "int8-split5", "bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
-        "int8-long", "bf16-tails", "int8-tails"])
+        "int8-long", "bf16-tails", "int8-tails", "bf16-one-range", "bf16-one-split", "bf16-one-split-new-block",
+        "bf16-one-range-d256"])
 def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part, lens):
     w = wl.make_small(70 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
                       kv_dtype=kv_dtype, q_dtype=q_dtype)
