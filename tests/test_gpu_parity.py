@@ -473,6 +473,8 @@ def test_decode_invalid_block_ids_read_as_zero(stream):
 # Positions T-1 with (T-1) % 16 == 0 start a block (fresh int8 statistics); the rest append mid-block.
 APPEND_LENS = [1, 2, 16, 17, 33, 100, 256, 257, 300, 513, 1000, 1024, 1025, 2000]
 TAIL_LENS = [16 * b + r for b in (0, 1, 2) for r in range(1, 17)]  # every position of the new token
+# more sequences than one persistent launch takes (2047): the call runs in chunks of sequences
+MANY_LENS = np.random.default_rng(83).integers(1, 60, size=2100).tolist()
 
 
 # Long rows: segments of up to 256 blocks (64 per wave), the appended block at a late lane;
@@ -488,9 +490,10 @@ LONG_LENS = [5000, 1, 4100, 3000, 17, 6000, 40000, 1025, 2049]
     (1, 1, 32, 8, 128, 0, TAIL_LENS), (2, 0, 32, 8, 128, 0, TAIL_LENS),
     # one range, no merge launch: the owning wave writes the token (V tile patched in LDS)
     (1, 1, 32, 8, 128, 0, [40]), (1, 0, 8, 2, 64, -1, [1000]), (1, 1, 8, 2, 128, -1, [33]), (1, 1, 16, 4, 256, 0, [64]),
+    (1, 1, 8, 2, 64, 0, MANY_LENS), (2, 0, 8, 2, 64, 0, MANY_LENS),
 ], ids=["bf16-split16", "int8-split5", "bf16-auto", "bf16-d64", "int8-auto", "int8-d256", "fp32-d64", "fp32-d128", "bf16-256", "bf16-long",
         "int8-long", "bf16-tails", "int8-tails", "bf16-one-range", "bf16-one-split", "bf16-one-split-new-block",
-        "bf16-one-range-d256"])
+        "bf16-one-range-d256", "bf16-many-seqs", "int8-many-seqs"])
 def test_decode_append_matches_append_then_decode(stream, kv_dtype, q_dtype, Hq, Hkv, D, part, lens):
     w = wl.make_small(70 + D + kv_dtype, num_seqs=len(lens), lens=lens, Hq=Hq, Hkv=Hkv, D=D,
                       kv_dtype=kv_dtype, q_dtype=q_dtype)
