@@ -133,7 +133,7 @@ struct PipeBufs {
 // Vector memory instructions load_block issues per block.
 template <int D, int KV>
 __host__ __device__ constexpr int decode_block_loads() {
-    return KV == PA_DTYPE_INT8 ? D / 64 + (D >= 64 ? D / 64 : D / 16) : D / 32 + D / 32;
+    return KV == PA_DTYPE_INT8 ? D / 64 + D / 64 : D / 32 + D / 32;
 }
 // s_waitcnt operand: wait until at most N vector memory operations are outstanding (no wait on
 // the other counters).
@@ -229,12 +229,6 @@ __device__ __forceinline__ void load_side(const DecodeArgs& a, const Piece& g, i
     }
 }
 
-// int8 caches with D >= 64 load V 16 bytes per lane (int8_v_transpose).
-template <int D, int KV>
-__host__ __device__ constexpr bool int8_wide_v() {
-    return KV == PA_DTYPE_INT8 && D >= 64;
-}
-
 // Tokens 4 tok_group(q4) .. + 3 of a block are the QK MFMA rows (S^T) and PV MFMA k values of lane
 // group q4. bf16 caches exchange groups 1 and 2 (bf16_v_exchange), so their K rows are loaded in
 // that order as well.
@@ -245,8 +239,8 @@ __device__ __forceinline__ int tok_group(int q4) {
 
 // Loads of block bid (K/V tile of KV head kv) into a pipeline buffer, lane (q4, n): K row n (the
 // lane's dims of each slab; bf16: row 4 tok_group(n / 4) + n % 4), V dim n of tokens 4q4 .. 4q4 + 3
-// (every 16th dim; bf16 and int8 with D >= 64: 16-byte loads whose words bf16_v_exchange() /
-// int8_v_transpose() put in that order, bf16 with tok_group). Loads go through
+// (every 16th dim; loaded 16 bytes per lane, the words put in that order by bf16_v_exchange() /
+// int8_v_transpose(), bf16 with tok_group). Loads go through
 // per-block buffer descriptors: bid < 0 (past a list, or an invalid id) gives a zero-sized
 // descriptor, so its loads return zeros without touching memory. The load sequence is therefore
 // identical on every iteration (no branches), which lets the compiler wait for exactly the oldest
@@ -255,9 +249,9 @@ template <int D, int KV>
 __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw<KV>::K (&kr)[D / 32],
                                            typename MfmaRaw<KV>::V (&vr)[D / 16], int bid, int kv) {
     using KR = typename MfmaRaw<KV>::K;
-    using VR = typename MfmaRaw<KV>::V;
     constexpr int ELT = MfmaRaw<KV>::kElt;
-    constexpr int NSLAB = D / 32, NT = D / 16, TILE = 16 * D;
+    constexpr int NSLAB = D / 32, TILE = 16 * D;
+    static_assert(KV != PA_DTYPE_INT8 || D >= 64, "int8 caches take head_dim 64, 128 or 256");
     // Cache policy: non-temporal for V (each tile is read once) and, for int8 caches, for K too
     // (bf16 K with it measured slower).
     constexpr int kCPK = KV == PA_DTYPE_INT8 ? kLoadNonTemporal : kLoadDefault;
@@ -266,7 +260,6 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
     const int q4 = lane >> 4, n = lane & 15;
     const int krow = KV == PA_DTYPE_BF16 ? 4 * tok_group<KV>(n >> 2) + (n & 3) : n;
     const int k_row_off = krow * D * ELT;            // K row krow; slab s of this lane starts at dim k_dim0(s, q4)
-    const int v_lane_off = (n * 16 + 4 * q4) * ELT;  // V dim n, tokens 4q4 .. (+16 dims per tile)
     const int64_t tile = bid >= 0 ? (static_cast<int64_t>(bid) * a.num_kv_heads + kv) * TILE * ELT : 0;
     const int bytes = bid >= 0 ? TILE * ELT : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -294,8 +287,8 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
             vr[2 * u] = make_uint2(w.x, w.y);
             vr[2 * u + 1] = make_uint2(w.z, w.w);
         }
-    } else if constexpr (int8_wide_v<D, KV>()) {
-        // int8, D >= 64: load u of lane (q4, n) is all 16 tokens of dim 16 (q4 + 4u) + n (one
+    } else {
+        // int8 (D >= 64): load u of lane (q4, n) is all 16 tokens of dim 16 (q4 + 4u) + n (one
         // contiguous KiB per instruction, a quarter of the instructions of 4-byte loads);
         // int8_v_transpose() turns words vr[4u .. 4u + 3] into tiles 4u .. 4u + 3.
 #pragma unroll
@@ -306,9 +299,6 @@ __device__ __forceinline__ void load_block(const DecodeArgs& a, typename MfmaRaw
             vr[4 * u + 2] = w.z;
             vr[4 * u + 3] = w.w;
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < NT; t++) vr[t] = buffer_load<VR, kCPV>(rv, v_lane_off + 256 * t * ELT);
     }
 }
 
@@ -576,10 +566,8 @@ __device__ __forceinline__ void mfma_piece(const DecodeArgs& a, const Piece& g, 
             if constexpr (KV == PA_DTYPE_INT8) p[i] *= vfac;
         }
         if constexpr (KV == PA_DTYPE_INT8) {
-            if constexpr (int8_wide_v<D, KV>()) {
 #pragma unroll
-                for (int u = 0; u < D / 64; u++) int8_v_transpose(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
-            }
+            for (int u = 0; u < D / 64; u++) int8_v_transpose(vr[4 * u], vr[4 * u + 1], vr[4 * u + 2], vr[4 * u + 3]);
             // int8 caches (bar 2e-2): one bf16 P, rounded to nearest even (relative error <= 2^-9;
             // v_cvt_pk_bf16_f32), half the PV MFMAs of the split below. p is finite and non-negative.
             uint32_t pr[2];
