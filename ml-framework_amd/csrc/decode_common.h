@@ -97,24 +97,69 @@ __device__ __forceinline__ float act_at(const void* p, bool f32, int64_t i) {
 // left dirty in the caches for the next step's reads to evict, those lines cost the C2 step 3-4 us
 // (measured: in the decode, in the merge kernel with plain stores, as whole tiles read and
 // rewritten; non-temporal 2-byte stores here cost the least).
-template <int D>
-__device__ __forceinline__ void append_token_bf16(const DecodeArgs& a, int seq, int kvh) {
-    // The length, then the table entry of the token's block (the values' loads go out with it).
+template <int D, bool F32>
+__device__ __forceinline__ void append_token_bf16_as(const DecodeArgs& a, int seq, int kvh) {
+    // Every load goes out before any is used: the length, the token's values and, for tables of up
+    // to kRowIds * 64 blocks, the sequence's table row, from which the token's block is picked; the
+    // stores then wait for one round trip instead of three (length, then table entry, then values).
+    constexpr int NPL = (D + 63) / 64;
+    constexpr int kRowIds = 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t src = (static_cast<int64_t>(seq) * a.num_kv_heads + kvh) * D;
+    uint32_t kraw[NPL], vraw[NPL];
+#pragma unroll
+    for (int e = 0; e < NPL; e++) {
+        const int d = lane + 64 * e;
+        kraw[e] = 0;
+        vraw[e] = 0;
+        if (d < D) {
+            if constexpr (F32) {
+                kraw[e] = static_cast<const uint32_t*>(a.k_new)[src + d];
+                vraw[e] = static_cast<const uint32_t*>(a.v_new)[src + d];
+            } else {
+                kraw[e] = static_cast<uint32_t>(static_cast<const uint16_t*>(a.k_new)[src + d]) << 16;
+                vraw[e] = static_cast<uint32_t>(static_cast<const uint16_t*>(a.v_new)[src + d]) << 16;
+            }
+        }
+    }
+    const int32_t* row = a.block_tables + static_cast<int64_t>(seq) * a.max_blocks_per_seq;
+    const bool whole_row = a.max_blocks_per_seq <= kRowIds * 64;
+    int ids[kRowIds];
+#pragma unroll
+    for (int k = 0; k < kRowIds; k++) {
+        const int b = lane + 64 * k;
+        ids[k] = whole_row && b < a.max_blocks_per_seq ? row[b] : -1;
+    }
     const int T = clamp_len(a, a.context_lens[seq]);
     if (T < 2) return;  // T == 1: the decode writes it (no streamed block); T <= 0: nothing
-    const int bid = a.block_tables[static_cast<int64_t>(seq) * a.max_blocks_per_seq + (T - 1) / 16];
+    const int bi = (T - 1) / 16;
+    int bid;
+    if (whole_row) {
+        int w = ids[0];
+#pragma unroll
+        for (int k = 1; k < kRowIds; k++) w = (bi >> 6) == k ? ids[k] : w;
+        bid = __builtin_amdgcn_readlane(w, bi & 63);
+    } else {
+        bid = row[bi];
+    }
     if (bid < 0 || bid >= a.num_blocks) return;
-    const int lane = threadIdx.x & 63, r = (T - 1) & 15;
-    const bool f32 = !a.q_bf16;
-    const int64_t src = (static_cast<int64_t>(seq) * a.num_kv_heads + kvh) * D;
+    const int r = (T - 1) & 15;
     const int64_t tile = (static_cast<int64_t>(bid) * a.num_kv_heads + kvh) * 16 * D;
     uint16_t* kc = static_cast<uint16_t*>(const_cast<void*>(a.k_cache)) + tile;
     uint16_t* vc = static_cast<uint16_t*>(const_cast<void*>(a.v_cache)) + tile;
 #pragma unroll
-    for (int d = lane; d < D; d += 64) {
-        __builtin_nontemporal_store(pa::bf16_trunc(act_at(a.k_new, f32, src + d)), kc + r * D + d);
-        __builtin_nontemporal_store(pa::bf16_trunc(act_at(a.v_new, f32, src + d)), vc + d * 16 + r);
+    for (int e = 0; e < NPL; e++) {
+        const int d = lane + 64 * e;
+        if (d < D) {
+            __builtin_nontemporal_store(pa::bf16_trunc(__uint_as_float(kraw[e])), kc + r * D + d);
+            __builtin_nontemporal_store(pa::bf16_trunc(__uint_as_float(vraw[e])), vc + d * 16 + r);
+        }
     }
+}
+template <int D>
+__device__ __forceinline__ void append_token_bf16(const DecodeArgs& a, int seq, int kvh) {
+    if (a.q_bf16) append_token_bf16_as<D, false>(a, seq, kvh);
+    else append_token_bf16_as<D, true>(a, seq, kvh);
 }
 
 // Final write of one (sequence, query head, dim): normalised output, or the partition's partial.
