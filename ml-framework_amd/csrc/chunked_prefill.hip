@@ -443,14 +443,21 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
         // |v| converted is kept in v_big and a round that met one is computed again exactly (see
         // the end of the round). The barrier before the pair is computed publishes the fp16 tiles.
         uint64_t v_big = 0;
+        // The wave's V chunks of the slot are all read before any is written back, so their LDS
+        // latencies overlap (written chunk by chunk, each read waited for the previous write).
         auto convert_v = [&](int slot) {
+            constexpr int NV = NSEG >= 2 ? NSEG / 2 : 1;
+            if (NSEG >= 2 || seg_v0) {
+                uint4* c[NV];
+                uint4 x[NV];
 #pragma unroll
-            for (int k = 0; k < NSEG; k++) {
-                if (NSEG >= 2 ? (k & 1) : seg_v0) {
-                    const int j = NSEG >= 2 ? k >> 1 : 0;
-                    uint4* c = s_tile + (TL::base(slot, seg_blk) + TL::K_CHUNKS + (seg_i0 + j) * 64 + lane);
-                    const uint4 x = *c;
-                    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+                for (int j = 0; j < NV; j++) {
+                    c[j] = s_tile + (TL::base(slot, seg_blk) + TL::K_CHUNKS + (seg_i0 + j) * 64 + lane);
+                    x[j] = *c[j];
+                }
+#pragma unroll
+                for (int j = 0; j < NV; j++) {
+                    const uint32_t w[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
                     uint32_t o[4];
                     float mx = 0.0f;
 #pragma unroll
@@ -460,7 +467,7 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                         o[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
                     }
                     v_big |= __builtin_amdgcn_ballot_w64(mx >= 65536.0f);  // 65536: the least bf16 above 65504
-                    *c = make_uint4(o[0], o[1], o[2], o[3]);
+                    *c[j] = make_uint4(o[0], o[1], o[2], o[3]);
                 }
             }
         };
@@ -568,7 +575,16 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
             // fp16: bf16 caches' tiles were converted in LDS when they landed, int8 codes are
             // converted here (exact). One PV MFMA per unit and 16-dim tile; bf16 row sums from one
             // more MFMA against ones, int8 row sums in l_run (P without the V scale). The P of both
-            // units first, then each V operand is read right before the MFMAs that use it.
+            // units first, then each V operand is read right before the MFMAs that use it, except
+            // (bf16 caches) the first two, read before the exponentials so that their LDS latency
+            // passes while those issue.
+            constexpr int NVPF = ELT == 2 ? 2 : 0;
+            uint4 vpf[NVPF > 0 ? NVPF : 1];
+            if constexpr (ELT == 2) {
+#pragma unroll
+                for (int t = 0; t < NVPF; t++)
+                    vpf[t] = *reinterpret_cast<const uint4*>(tv + TL::vpos(16 * t + n, q4 >> 1, pblk) * 16);
+            }
             f16x8_t pf[2];
 #pragma unroll
             for (int k = 0; k < 2; k++) {
@@ -598,7 +614,8 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
                 const int d = 16 * t + n;
                 f16x8_t vop;
                 if constexpr (ELT == 2) {
-                    vop = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
+                    if (t < NVPF) vop = __builtin_bit_cast(f16x8_t, vpf[t < NVPF ? t : 0]);
+                    else vop = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4*>(tv + TL::vpos(d, q4 >> 1, pblk) * 16));
                 } else {
                     const uint2 c = *reinterpret_cast<const uint2*>(tv + TL::vpos(d, 0, pblk) * 16 + (q4 >> 1) * 8);
                     uint32_t o[4];
