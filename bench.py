@@ -48,6 +48,7 @@ METRIC = "paged decode HBM GB/s (% peak) + tokens/s per layer, Llama-3-8B shape,
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
 GATE_CLOCKS_PER_US = 2500  # the timer's spin: shader clocks per us, above MI355X's 2.4 GHz top clock
+GATE_MAX_SPIN_US = 2000.0
 # HBM traffic of the headline call measured with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE per
 # dispatch, scaled by the same counters' reading for a plain copy of known size); written by the
 # profiling summary, absent until then.
@@ -124,9 +125,10 @@ class Timer:
 
     With `gate` (the default) the timed calls are queued behind a gate: after the synchronize,
     a spin kernel on torch's stream that the library's stream waits for, long enough for the host
-    to enqueue all `steps` calls (twice the host's measured enqueue time per call, plus 200 us; the
-    spin counts shader clocks, converted at 2.5 GHz, above the chip's top clock, so that it lasts
-    at least that long at any clock).
+    to enqueue all `steps` calls (twice the host's measured enqueue time per call, plus 200 us, at
+    most 2 ms; the spin counts shader clocks, converted at 2.5 GHz, above the chip's top clock, so
+    that it lasts at least that long at any clock). The MFMA-bound prefill legs are timed without
+    the gate: after an idle spell the chip's clocks drop and that kernel runs slower for a while.
     The start event is then taken when the GPU begins the first timed call rather than when the
     host begins issuing it, so a short run measures the same per-step rate as a long one: without
     the gate, the first call of a run waits for its own launch from Python (about 10 us of host
@@ -156,7 +158,8 @@ class Timer:
             if self._torch_stream is None:
                 self._torch_stream = pa.TorchStream.current(0).stream
             g0, g1 = pa.Event(self.dev), pa.Event(self.dev)
-            spin_us = 200.0 + 2.0 * steps * host_per_call_us
+            # at most 2 ms: a longer idle spin lets the clocks drop before the timed calls
+            spin_us = min(200.0 + 2.0 * steps * host_per_call_us, GATE_MAX_SPIN_US)
             t_host = time.perf_counter()
             g0.record(self._torch_stream)
             torch.cuda._sleep(int(spin_us * GATE_CLOCKS_PER_US))
@@ -342,8 +345,9 @@ def run_c3(timer, stream, steps, warmup, seed):
 
     ms_dec = timer(dec, steps, warmup)
     ms_app = timer(app, steps, warmup)
-    ms_pre = timer(pre, steps, max(warmup, PREFILL_WARMUP_CALLS))
-    ms_step = timer(step, steps, max(warmup, PREFILL_WARMUP_CALLS))
+    # the MFMA-bound prefill runs at lower clocks after an idle spell, so its legs are timed ungated
+    ms_pre = timer(pre, steps, max(warmup, PREFILL_WARMUP_CALLS), gate=False)
+    ms_step = timer(step, steps, max(warmup, PREFILL_WARMUP_CALLS), gate=False)
     flops = float(4 * w.num_q_heads * w.head_dim * np.sum(L * P + L * (L + 1) / 2))
     pre_kv_bytes = float(np.sum(P + L)) * w.kv_bytes_per_token()
     dec_bytes = w.decode_algorithmic_bytes() + append_bytes(w)
@@ -615,7 +619,7 @@ def main():
     timer = Timer(dev, stream)
     if args.only_prefill:
         w3, _, _, pre, P, L, _ = c3_setup(stream, 3)
-        ms = timer(pre, args.steps, max(args.warmup, PREFILL_WARMUP_CALLS))
+        ms = timer(pre, args.steps, max(args.warmup, PREFILL_WARMUP_CALLS), gate=False)
         flops = float(4 * w3.num_q_heads * w3.head_dim * np.sum(P * L + L * (L + 1) / 2))
         print(json.dumps({"mode": "only-prefill", "workload": "C3 chunked prefill", "us": round(ms * 1e3, 3),
                           "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "steps": args.steps}), flush=True)
