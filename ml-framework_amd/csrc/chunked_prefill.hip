@@ -576,9 +576,10 @@ __global__ __launch_bounds__(kPrefillThreads, D > 128 ? 1 : (D > 64 && QF32 ? 2 
             // converted here (exact). One PV MFMA per unit and 16-dim tile; bf16 row sums from one
             // more MFMA against ones, int8 row sums in l_run (P without the V scale). The P of both
             // units first, then each V operand is read right before the MFMAs that use it, except
-            // (bf16 caches) the first two, read before the exponentials so that their LDS latency
-            // passes while those issue.
-            constexpr int NVPF = ELT == 2 ? 2 : 0;
+            // (bf16 caches) the first one, read before the exponentials so that its LDS latency
+            // passes while those issue (two measured slower: the extra operand's registers cost
+            // moves).
+            constexpr int NVPF = ELT == 2 ? 1 : 0;
             uint4 vpf[NVPF > 0 ? NVPF : 1];
             if constexpr (ELT == 2) {
 #pragma unroll
